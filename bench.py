@@ -1,0 +1,253 @@
+#!/usr/bin/env python3
+"""Hot-expert MoE layer benchmark on one MI355X.
+
+Headline: tokens/s of one hot-expert MoE layer at a 16384-token prefill chunk (hidden 2048,
+expert intermediate 512, 256 experts, top-8, 40 hot slots, Q4_K gate/up + Q6_K down, Zipf
+1.1 routing), inputs resident in HBM. A step is one layer forward (route sort, gate/up
+GEMM with SiLU*mul, down GEMM, weighted combine) over the chunk. Prints ONE JSON line.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-decode]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import importlib.util
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+HEADLINE = "q4_k+q6_k-h2048-n512-e256-k8-hot40-prefill"
+DECODE = "q4_k-h2048-n512-e256-k8-hot32-decode"
+STAGES = ["prep", "gate_up", "mid", "down", "combine"]
+
+
+def load_pkg():
+    name = "kt_prefill_lend_amd"
+    if name in sys.modules:
+        return sys.modules[name]
+    root = ROOT / "kt-prefill-lend_amd"
+    spec = importlib.util.spec_from_file_location(name, root / "__init__.py", submodule_search_locations=[str(root)])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+class HipEvents:
+    """hipEvent_t handles through libamdhip64 (events on the stream the kernels run on)."""
+
+    def __init__(self):
+        self.h = C.CDLL("libamdhip64.so")
+        self.h.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+        self.h.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
+        self.h.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+        self.h.hipEventSynchronize.argtypes = [C.c_void_p]
+        self.h.hipEventDestroy.argtypes = [C.c_void_p]
+
+    def create(self, n):
+        out = (C.c_void_p * n)()
+        for i in range(n):
+            e = C.c_void_p()
+            assert self.h.hipEventCreate(C.byref(e)) == 0
+            out[i] = e
+        return out
+
+    def record(self, e, stream):
+        assert self.h.hipEventRecord(e, stream) == 0
+
+    def ms(self, a, b):
+        f = C.c_float()
+        assert self.h.hipEventElapsedTime(C.byref(f), a, b) == 0
+        return f.value
+
+    def destroy(self, evs):
+        for e in evs:
+            self.h.hipEventDestroy(e)
+
+
+def log(msg):
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
+def time_layer(P, torch, desc_list, x, w, slot, mode, steps, warmup, ev: HipEvents):
+    """Warmup, then `steps` timed layer calls. desc_list rotates weight copies per step.
+    Returns (ms per step, per-stage mean ms)."""
+    H, L = P.kt_gguf_hot, P._lib
+    lib = L.lib()
+    T, k = slot.shape
+    out = torch.empty((T, desc_list[0].hidden), dtype=torch.bfloat16, device=x.device)
+    need = max(lib.ktmi_moe_layer_workspace(d, T, k, mode) for d in desc_list)
+    ws = torch.empty((need,), dtype=torch.uint8, device=x.device)
+    stream = L.stream_ptr(x.device)
+    for i in range(warmup):
+        H.moe_layer(desc_list[i % len(desc_list)], x, w, slot, mode, out, ws)
+    stage_ev = ev.create(steps * L.STAGE_EVENTS)
+    se = ev.create(2)
+    torch.cuda.synchronize()
+    ev.record(se[0], stream)
+    for i in range(steps):
+        arr = (C.c_void_p * L.STAGE_EVENTS)(*stage_ev[i * L.STAGE_EVENTS:(i + 1) * L.STAGE_EVENTS])
+        L.check(lib.ktmi_set_stage_events(arr, L.STAGE_EVENTS))
+        H.moe_layer(desc_list[i % len(desc_list)], x, w, slot, mode, out, ws)
+    ev.record(se[1], stream)
+    L.check(lib.ktmi_set_stage_events(None, 0))
+    torch.cuda.synchronize()
+    total = ev.ms(se[0], se[1])
+    per = np.zeros((steps, len(STAGES)))
+    for i in range(steps):
+        b = i * L.STAGE_EVENTS
+        for s in range(len(STAGES)):
+            per[i, s] = ev.ms(stage_ev[b + s], stage_ev[b + s + 1])
+    ev.destroy(stage_ev)
+    ev.destroy(se)
+    return total / steps, dict(zip(STAGES, per.mean(axis=0).tolist())), out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--tokens", type=int, default=16384)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--cpu-tokens", type=int, default=256, help="tokens of the chunk timed on the CPU")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported (this build has no multi-GPU "
+              f"path: the layer would shard by expert, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    P = load_pkg()
+    import kt_prefill_lend_amd.kt_gguf_hot  # noqa: F401
+    import kt_prefill_lend_amd.synth as S
+
+    dev = torch.device("cuda", 0)
+    ev = HipEvents()
+    w = S.WORKLOADS[HEADLINE]
+    T = args.tokens
+    t0 = time.time()
+    ids, tw, slot, hot = S.routing(w, T)
+    xb = S.activations(w, T)
+    w13, w2 = S.slot_tensors(w)
+    log(f"workload {w.name} T={T}: generated in {time.time() - t0:.1f}s, hot routes {(slot >= 0).sum()}")
+    x = torch.from_numpy(xb.view(np.int16)).to(dev).view(torch.bfloat16)
+    tw_d = torch.from_numpy(tw).to(dev)
+    slot_d = torch.from_numpy(slot).to(dev)
+    W13 = torch.from_numpy(w13).to(dev)
+    W2 = torch.from_numpy(w2).to(dev)
+    H, L = P.kt_gguf_hot, P._lib
+    desc = H.layer_desc(W13, W2, w.hidden, w.inter, w.types[0], w.types[2])
+    ms, stages, out = time_layer(P, torch, [desc], x, tw_d, slot_d, L.MODE_GROUPED, args.steps, args.warmup, ev)
+    r_hot = int((slot >= 0).sum())
+    flop_gu = 4.0 * w.hidden * w.inter * r_hot
+    flop_dn = 2.0 * w.hidden * w.inter * r_hot
+    kern = {"gate_up": (flop_gu, stages["gate_up"]), "down": (flop_dn, stages["down"])}
+    dom = max(kern, key=lambda k: kern[k][1])
+    achieved = kern[dom][0] / (kern[dom][1] * 1e-3) / 1e12
+    tok_s = T / (ms * 1e-3)
+    layer_tflops = (flop_gu + flop_dn) / (ms * 1e-3) / 1e12
+    log(f"layer {ms:.3f} ms/step, {tok_s / 1e6:.2f} M tok/s, {layer_tflops:.0f} TFLOP/s "
+        f"({100 * layer_tflops / PEAK_BF16_TFLOPS:.1f}% of bf16 peak); stages ms {stages}")
+
+    traffic = None
+    tfile = ROOT / "profiles" / "traffic.json"
+    if tfile.exists():
+        try:
+            tj = json.loads(tfile.read_text())
+            traffic = tj.get(f"{HEADLINE}:T{T}:{dom}")
+        except Exception:  # noqa: BLE001
+            traffic = None
+
+    result = {
+        "metric": "hot-expert MoE layer tokens/s @16K chunk; % of HBM/MFMA roofline",
+        "value": round(tok_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) experts quantised to GGUF, Zipf(1.1) routing)",
+        "config": {"workload": w.name, "tokens": T, "hidden": w.hidden, "inter": w.inter, "experts": w.experts,
+                   "top_k": w.top_k, "hot_slots": w.hot, "types": "Q4_K gate/up, Q6_K down", "hot_routes": r_hot,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+                     "layer_frac": round(layer_tflops / PEAK_BF16_TFLOPS, 4),
+                     "stage_ms": {k: round(v, 4) for k, v in stages.items()}},
+        "cpu_baseline": None,
+    }
+
+    if not args.no_decode:
+        result["decode"] = bench_decode(P, torch, S, ev, dev)
+
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(S, w, args.cpu_tokens, T)
+
+    print(json.dumps(result), flush=True)
+
+
+def bench_decode(P, torch, S, ev, dev, steps=50, warmup=5):
+    """Decode-shaped layer (Q4_K, 32 hot slots) at 1/4/8/16 tokens: GB/s against HBM with the
+    weights rotated over enough copies to exceed the 256 MB Infinity Cache."""
+    H, L = P.kt_gguf_hot, P._lib
+    w = S.WORKLOADS[DECODE]
+    w13, w2 = S.slot_tensors(w)
+    per_copy = w13.nbytes + w2.nbytes
+    ncopy = max(8, int(np.ceil(600e6 / per_copy)))
+    W13 = torch.from_numpy(w13).to(dev)
+    W2 = torch.from_numpy(w2).to(dev)
+    copies = [(W13.clone(), W2.clone()) for _ in range(ncopy)]
+    descs = [H.layer_desc(a, b, w.hidden, w.inter, w.types[0], w.types[2]) for a, b in copies]
+    res = {}
+    from kt_prefill_lend_amd.gguf import row_bytes
+
+    exp_bytes = 2 * w.inter * row_bytes(w.hidden, w.types[0]) + w.hidden * row_bytes(w.inter, w.types[2])
+    for T in w.tokens:
+        ids, tw, slot, _ = S.routing(w, T)
+        x = torch.from_numpy(S.activations(w, T).view(np.int16)).to(dev).view(torch.bfloat16)
+        tw_d, slot_d = torch.from_numpy(tw).to(dev), torch.from_numpy(slot).to(dev)
+        uniq = len(set(slot[slot >= 0].tolist()))
+        nbytes = uniq * exp_bytes + 2 * T * w.hidden * 2
+        out = {}
+        for name, dl in (("hbm", descs), ("warm", descs[:1])):
+            ms, stages, _ = time_layer(P, torch, dl, x, tw_d, slot_d, L.MODE_GEMV, steps, warmup, ev)
+            kern = sum(stages.values())
+            out[name] = {"ms_per_step": round(ms, 4), "kernels_ms": round(kern, 4),
+                         "GBps_kernels": round(nbytes / (kern * 1e-3) / 1e9, 1),
+                         "frac_hbm": round(nbytes / (kern * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                         "stage_ms": {k: round(v, 4) for k, v in stages.items()}}
+        res[f"T{T}"] = {"hot_routes": int((slot >= 0).sum()), "unique_experts": uniq, "bytes": nbytes, **out}
+        log(f"decode T={T}: {res[f'T{T}']}")
+    del copies
+    return res
+
+
+def cpu_baseline(S, w, cpu_tokens, T):
+    """The CPU expert path (a C restatement of kt-kernel's forward_many) on the same
+    workload's first `cpu_tokens` tokens, hot routes only, on this host's cores."""
+    try:
+        sys.path.insert(0, str(ROOT))
+        from oracle import cpu_moe
+    except Exception as e:  # noqa: BLE001
+        log(f"cpu baseline unavailable: {e}")
+        return None
+    return cpu_moe.bench(S, w, cpu_tokens, T, log)
+
+
+if __name__ == "__main__":
+    main()

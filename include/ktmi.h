@@ -1,0 +1,155 @@
+/* ktmi: MI355X (gfx950) hot-expert MoE for GGUF experts -- the C ABI.
+ *
+ * Every entry point takes plain pointers (device pointers unless stated otherwise),
+ * sizes and a HIP stream passed as `void*` (NULL = the default stream), returns an int
+ * status (KTMI_OK or a negative KTMI_E* code) and never synchronises the stream. After a
+ * failure ktmi_last_error() describes it (thread-local). Nothing here allocates device
+ * memory except where stated (the streamer's device slots): scratch comes in through a
+ * caller-provided workspace whose size the matching *_workspace() call returns.
+ *
+ * Citations name the reference interface each entry replaces; paths are relative to the
+ * reference repository, P:<n> is line n of
+ * trees/flash-next-gguf/sglang-v0.5.19-flash-next-gguf.patch.
+ */
+#ifndef KTMI_H
+#define KTMI_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KTMI_OK 0
+#define KTMI_EINVAL (-1) /* bad shape, pointer or argument */
+#define KTMI_ETYPE (-2)  /* ggml type without a kernel here */
+#define KTMI_EHIP (-3)   /* a HIP runtime call failed */
+#define KTMI_ESPACE (-4) /* workspace smaller than required */
+
+/* activation / output element types */
+#define KTMI_F32 0
+#define KTMI_F16 1
+#define KTMI_BF16 2
+
+/* ggml type ids with kernels: Q8_0 = 8, Q4_K = 12, Q6_K = 14, IQ3_S = 21 */
+
+/* layer modes for ktmi_moe_layer */
+#define KTMI_MODE_AUTO 0
+#define KTMI_MODE_GEMV 1    /* decode windows: int8 dot-product GEMV over raw blocks */
+#define KTMI_MODE_GROUPED 2 /* prefill chunks: routes sorted by slot, dequant-in-LDS bf16 MFMA */
+
+/* Thread-local text of the last failure ("" if none). */
+const char* ktmi_last_error(void);
+
+/* Library version (major*10000 + minor*100 + patch). */
+int ktmi_version(void);
+
+/* 1 if `ggml_type` has kernels here, else 0. Replaces the MMVQ_TYPES / DENSE_TYPES
+ * membership checks of hot/kt_gguf_hot.py:81,187-190 and hot/kt_gguf_moe_multi.py:49. */
+int ktmi_type_supported(int ggml_type);
+
+/* Bytes of one row of `cols` values of `ggml_type`; 0 if cols is not a multiple of the
+ * block size or the type is unknown. hot/kt_gguf_hot.py:88-91 (_row_bytes). */
+int64_t ktmi_row_bytes(int64_t cols, int ggml_type);
+
+/* ---- activation quantisation (q8_1) ---------------------------------------------
+ * Bytes of one q8_1 row: cols padded to a multiple of 512, 36 bytes per 32 values.
+ * kt_gguf_moe_multi.cu:664-668 (quant_X allocation). */
+int64_t ktmi_q8_1_row_bytes(int64_t cols);
+/* x [tokens, cols] (x_dtype) -> q8_1 blocks [tokens, ktmi_q8_1_row_bytes(cols)]:
+ * d = amax/127, q = roundf(x/d), ds = (half d, half sum). hot/kt_gguf_moe_multi/
+ * kt_gguf_moe_multi.cu:600-650 (quantize_q8_1, quantize_row_q8_1_cuda). */
+int ktmi_quantize_q8_1(const void* x, int x_dtype, int64_t cols, int64_t tokens, void* out, void* stream);
+
+/* ---- the GGUF MoE GEMV (decode windows) -------------------------------------------
+ * Y[p, r] = sum over the blocks of row r of expert ids[p] of the int8 dot products
+ * against q8_1(X[p / top_k]), for every route p < tokens*top_k; ids[p] < 0 gives a zero
+ * row. per_route = 0: the first route of each expert computes every route of that
+ * expert (one read of its weights per call); per_route = 1: each route alone. The sums
+ * are the same in both. W: w_is_table = 0 -> slot tensor uint8 [E, rows, row_bytes(cols)];
+ * w_is_table = 1 -> int64 [E] device table of per-slot row-0 addresses.
+ * Y [tokens*top_k, rows] in x_dtype. Workspace: ktmi_moe_a8_vec_workspace(cols, tokens).
+ * Replaces torch::Tensor kt_moe_a8_vec_multi(X, W, topk_ids, top_k, type, row, tokens)
+ * (hot/kt_gguf_moe_multi/kt_gguf_moe_multi.cu:653-935) in both its window build and its
+ * KT_PER_ROUTE / KT_PTR_TABLE builds (hot/kt_gguf_moe_multi.py:55-87). */
+int64_t ktmi_moe_a8_vec_workspace(int64_t cols, int64_t tokens);
+int ktmi_moe_a8_vec(const void* X, int x_dtype, int64_t cols, const void* W, int w_is_table,
+                    const int32_t* ids, int64_t top_k, int ggml_type, int64_t rows, int64_t tokens,
+                    int per_route, void* Y, void* workspace, int64_t ws_bytes, void* stream);
+
+/* ---- dequantisation ---------------------------------------------------------------
+ * raw: n experts, raw_stride bytes apart, each rows*row_bytes(cols) bytes of blocks;
+ * out: bf16 [n, rows, cols], out_stride elements between experts, rows contiguous.
+ * Replaces dequant_experts(raw, raw_stride, type_id, n, rows, cols, out)
+ * (P:11471-11498; _iq3_s_kernel P:11397-11420) and extends it to Q8_0, Q4_K, Q6_K. */
+int ktmi_dequant_experts(const void* raw, int64_t raw_stride, int ggml_type, int64_t n, int64_t rows,
+                         int64_t cols, void* out_bf16, int64_t out_stride, void* stream);
+
+/* ---- hot-expert registry lookups -------------------------------------------------
+ * For one layer: slot_ids[i] = log2slot[ids[i]], cpu_ids[i] = log2cpu[ids[i]],
+ * counts[ids[i]] += 1 (fp32, exact for counts < 2^24), i < n; ids must lie in [0, E).
+ * Any n (the reference's fused kernel takes <= 64 routes, then falls back to torch).
+ * Replaces HotCache.route (hot/kt_hot_cache.py:121-143) and _route_kernel (:62-75). */
+int ktmi_hot_route(const int32_t* ids, int64_t n, const int32_t* log2slot, const int32_t* log2cpu,
+                   float* counts, int32_t* slot_ids, int32_t* cpu_ids, void* stream);
+
+/* ---- epilogues ---------------------------------------------------------------------
+ * h [R, 2N] (rows [gate | up]) -> out [R, N] = silu(gate) * up, fp32 maths, one rounding.
+ * Replaces sgl_kernel.silu_and_mul (call at hot/kt_gguf_hot.py:260). */
+int ktmi_silu_and_mul(const void* h, int dtype, int64_t R, int64_t N, void* out, void* stream);
+
+/* res[t] = round( sum_{k ascending} fp32( round( out[t,k] * round(w[t,k]) ) ) ), where
+ * round() is to `dtype` (bf16/f16) and the sum is fp32. out [T, top_k, K], w fp32 [T, top_k].
+ * Replaces _combine (hot/kt_gguf_hot.py:43-71) and out.mul_(w) + moe_sum (:300-304). */
+int ktmi_combine(const void* out, int dtype, const float* w, int64_t T, int64_t top_k, int64_t K,
+                 void* res, void* stream);
+
+/* ---- one hot-expert MoE layer -----------------------------------------------------
+ * The GPU half of a layer: routes (t, k) with slot_ids[t*top_k+k] >= 0 run the expert in
+ * that slot; y[t] = combine over k of (silu(x_t Wg^T) * (x_t Wu^T)) Wd^T * w[t,k], cold
+ * routes (< 0, the CPU's) contribute nothing. Deterministic (no atomics on outputs).
+ * w13: slot tensor uint8 [n_slots, 2*inter, row_bytes(hidden, type13)], rows [gate; up];
+ * w2: uint8 [n_slots, hidden, row_bytes(inter, type2)]; with w_is_table = 1 both are int64
+ * device tables of per-slot addresses. x, y bf16 [tokens, hidden]; topk_w fp32.
+ * Replaces KTGGUFHotExpertsMethod.apply (hot/kt_gguf_hot.py:240-304) and the streamer's
+ * per-group dequant + cutlass_fused_moe body (P:40789-40819). */
+typedef struct ktmi_layer {
+  int64_t hidden;  /* K */
+  int64_t inter;   /* N, the expert intermediate size (this rank's part) */
+  int64_t n_slots; /* E_gpu, hot-expert slots */
+  int32_t type13;  /* ggml type of gate and up */
+  int32_t type2;   /* ggml type of down */
+  const void* w13;
+  const void* w2;
+  int32_t w_is_table;
+  int32_t reserved;
+} ktmi_layer;
+
+int64_t ktmi_moe_layer_workspace(const ktmi_layer* layer, int64_t tokens, int64_t top_k, int mode);
+int ktmi_moe_layer(const ktmi_layer* layer, const void* x, const float* topk_w, const int32_t* slot_ids,
+                   int64_t tokens, int64_t top_k, void* y, void* workspace, int64_t ws_bytes, int mode,
+                   void* stream);
+/* The mode KTMI_MODE_AUTO picks for this many routes. */
+int ktmi_moe_layer_mode(const ktmi_layer* layer, int64_t tokens, int64_t top_k);
+
+/* Stage timing for benchmarks (no counterpart in the reference, whose per-layer timers are
+ * host-side, P:40981-40985). events: KTMI_STAGE_EVENTS hipEvent_t handles that the next
+ * ktmi_moe_layer calls on this thread record on their stream at the stage boundaries:
+ * [0] start, [1] gate/up start (after route sort or x quantisation), [2] gate/up end,
+ * [3] down start (after SiLU*mul + q8_1 on the GEMV path), [4] down end, [5] combine end.
+ * events = NULL or n = 0 turns it off. */
+#define KTMI_STAGE_EVENTS 6
+int ktmi_set_stage_events(void* const* events, int n);
+
+/* ---- host-side GGUF quantisers (CPU) --------------------------------------------
+ * x fp32 [rows, cols] (host) -> blocks [rows, row_bytes(cols, type)] (host), using
+ * `threads` CPU threads (<= 0: all). Q8_0 d = amax/127; Q4_K/Q6_K per-sub-block range
+ * scales; IQ3_S nearest codebook point per 4-value group. Used to build expert weights;
+ * the GGUF files the reference loads are produced by llama.cpp's quantisers. */
+int ktmi_quantize_rows_host(const float* x, int64_t rows, int64_t cols, int ggml_type, void* out, int threads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KTMI_H */

@@ -1,0 +1,429 @@
+// Grouped hot-expert MoE for prefill chunks (gfx950: wave64, bf16 MFMA, 160 KB LDS).
+//
+//   1. sort_count / sort_scan / sort_scatter: a stable counting sort of the routes by
+//      slot (ascending route index inside a slot, cold routes dropped). Each wave owns a
+//      chunk of CHW consecutive routes; per-chunk histograms are scanned per slot, so
+//      every route's position is a pure function of the ids: no host sync, no atomics
+//      on positions, graph-capturable.
+//   2. gemm<GATEUP>: for each (slot, tile of BM sorted routes, tile of N) the gathered
+//      bf16 rows of x times the slot's gate and up rows, dequantised from raw GGUF blocks
+//      into LDS (bf16, RNE of the exact fp32 dequant value), on
+//      v_mfma_f32_32x32x16_bf16; the epilogue applies silu(gate)*up and writes bf16 rows
+//      of H in sorted order.
+//   3. gemm<down>: H rows (contiguous in sorted order) times the slot's down rows; the
+//      epilogue scatters bf16 rows to Y in route order (p = t*top_k + k).
+//   4. combine_routes: res[t] = sum over k ascending of bf16(Y[p] * bf16(w)), fp32, one
+//      rounding (the reference's _combine order), skipping cold routes.
+//
+// Reference: the streamer's per-group dequant + cutlass_fused_moe + acc.add_ (P:40789-40819,
+// dequant P:11471-11498), _combine (hot/kt_gguf_hot.py:43-71); the sort-by-expert follows the
+// idea of moe_prepare_ids_kernel (P:31142-31162) with a deterministic stable order.
+#include "formats.h"
+#include "kernels.h"
+
+namespace ktmi {
+
+namespace {
+
+constexpr int CHW = 1024;        // routes per wave chunk in the sort
+constexpr int SORT_THREADS = 256;
+constexpr int MAX_SLOTS = 512;
+
+// tile configuration
+constexpr int BK = 64;
+constexpr int PITCH = BK + 8;  // bf16 elements per LDS row (16-byte pad against bank conflicts)
+constexpr int FM = 2, FN = 2, WM = 2, WN = 2;
+constexpr int NTHREADS = WM * WN * 64;
+constexpr int BM = WM * FM * 32;   // routes per tile
+constexpr int BNW = WN * FN * 32;  // weight rows per tile (gate+up for GATEUP)
+
+__global__ __launch_bounds__(SORT_THREADS) void sort_count(const int32_t* __restrict__ slot_ids, int64_t R, int S,
+                                                           int32_t* __restrict__ hist, int64_t nch) {
+  __shared__ int cnt[SORT_THREADS / 64][MAX_SLOTS];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t ch = (int64_t)blockIdx.x * (SORT_THREADS / 64) + w;
+  for (int e = lane; e < S; e += 64) cnt[w][e] = 0;
+  __syncthreads();
+  if (ch < nch) {
+    const int64_t p0 = ch * CHW;
+    for (int i = lane; i < CHW; i += 64) {
+      const int64_t p = p0 + i;
+      if (p < R) {
+        const int e = slot_ids[p];
+        if (e >= 0 && e < S) atomicAdd(&cnt[w][e], 1);
+      }
+    }
+  }
+  __syncthreads();
+  if (ch < nch)
+    for (int e = lane; e < S; e += 64) hist[ch * S + e] = cnt[w][e];
+}
+
+// one workgroup: per-slot exclusive prefix over chunks (in place), then slot offsets
+// seg[S+1] and tile offsets tseg[S+1] (tiles of BM routes)
+__global__ __launch_bounds__(SORT_THREADS) void sort_scan(int32_t* __restrict__ hist, int64_t nch, int S,
+                                                          int32_t* __restrict__ seg, int32_t* __restrict__ tseg,
+                                                          int bm) {
+  __shared__ int tot[MAX_SLOTS];
+  __shared__ int til[MAX_SLOTS];
+  for (int e = threadIdx.x; e < S; e += blockDim.x) {
+    int run = 0;
+    for (int64_t c = 0; c < nch; ++c) {
+      const int v = hist[c * S + e];
+      hist[c * S + e] = run;
+      run += v;
+    }
+    tot[e] = run;
+    til[e] = (run + bm - 1) / bm;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int a = 0, b = 0;
+    for (int e = 0; e < S; ++e) {
+      seg[e] = a;
+      tseg[e] = b;
+      a += tot[e];
+      b += til[e];
+    }
+    seg[S] = a;
+    tseg[S] = b;
+  }
+}
+
+__global__ __launch_bounds__(SORT_THREADS) void sort_scatter(const int32_t* __restrict__ slot_ids, int64_t R, int S,
+                                                             const int32_t* __restrict__ hist, int64_t nch,
+                                                             const int32_t* __restrict__ seg,
+                                                             int32_t* __restrict__ perm) {
+  __shared__ int run[SORT_THREADS / 64][MAX_SLOTS];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t ch = (int64_t)blockIdx.x * (SORT_THREADS / 64) + w;
+  if (ch >= nch) return;  // whole wave; no block-wide barrier below
+  for (int e = lane; e < S; e += 64) run[w][e] = seg[e] + hist[ch * S + e];
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
+  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  const int64_t p0 = ch * CHW;
+  for (int it = 0; it < CHW; it += 64) {
+    const int64_t p = p0 + it + lane;
+    int e = -1;
+    if (p < R) {
+      e = slot_ids[p];
+      if (e >= S) e = -1;
+    }
+    const bool hot = e >= 0;
+    // lanes holding the same slot id: intersect ballots over the id's bits
+    uint64_t same = __ballot(hot);
+#pragma unroll
+    for (int b = 0; b < 10; ++b) {
+      const bool bit = (e >> b) & 1;
+      const uint64_t bb = __ballot(bit);
+      same &= bit ? bb : ~bb;
+    }
+    int base = 0;
+    if (hot) base = run[w][e];
+    __builtin_amdgcn_wave_barrier();
+    if (hot) {
+      const int rank = __popcll(same & lt);
+      perm[base + rank] = (int32_t)p;
+      if ((same & lt) == 0) run[w][e] = base + __popcll(same);  // lowest lane of the group
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + __expf(-g)) * u; }
+
+// GATEUP = true : A = x rows gathered through perm (token = p / top_k), Kdim = hidden,
+//                 B rows = [gate n0..n0+BNW/2 ; up NI+n0..], out = H [R, NI] sorted rows.
+// GATEUP = false: A = H rows m0.., Kdim = inter, B rows = down rows c0..c0+BNW,
+//                 out = Y [routes, NI] at row perm[m] (NI = hidden).
+template <int TYPE, bool GATEUP>
+__global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restrict__ A_src,
+                                                         const int32_t* __restrict__ perm,
+                                                         const int32_t* __restrict__ seg,
+                                                         const int32_t* __restrict__ tseg, int S, int top_k,
+                                                         const uint8_t* __restrict__ W, int w_is_table,
+                                                         int64_t w_expert_stride, int64_t rb, int Kdim, int NI,
+                                                         int NT, int64_t nblk, uint16_t* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) uint16_t As[BM * PITCH];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[BNW * PITCH];
+  __shared__ uint32_t grid_lds[TYPE == GGML_IQ3_S ? 512 : 1];
+
+  // XCD-aware order: workgroups are dealt to the 8 XCDs round-robin (pid % 8). All NT
+  // N tiles of one M tile go to the same XCD, so they share its L2 for the gathered A
+  // rows; M tiles rotate over the XCDs, so the real tiles (a prefix of the M range, the
+  // rest exit at once) spread evenly. gridDim.x is a multiple of 8 * NT.
+  const int64_t pid = blockIdx.x;
+  const int64_t idx = pid >> 3;
+  const int mt = (int)((idx / NT) * 8 + (pid & 7));
+  const int nt = (int)(idx % NT);
+  if ((int64_t)mt * NT + nt >= nblk) return;
+  const int total_tiles = tseg[S];
+  if (mt >= total_tiles) return;
+  int lo = 0, hi = S;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (tseg[mid] <= mt) lo = mid; else hi = mid;
+  }
+  const int e = lo;
+  const int m0 = seg[e] + (mt - tseg[e]) * BM;
+  const int valid = min(BM, seg[e + 1] - m0);
+
+  if constexpr (TYPE == GGML_IQ3_S) stage_iq3s_grid(grid_lds);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const uint8_t* wexp = w_is_table ? (const uint8_t*)((const int64_t*)W)[e] : W + (int64_t)e * w_expert_stride;
+
+  // ---- per-thread global sources (fixed over the K loop)
+  constexpr int CH_A = BM * (BK / 8) / NTHREADS;   // 16-byte pieces of A per thread
+  constexpr int CH_B = BNW * (BK / 16) / NTHREADS; // 16-value pieces of B per thread
+  const uint16_t* a_ptr[CH_A];
+#pragma unroll
+  for (int i = 0; i < CH_A; ++i) {
+    const int c = tid + NTHREADS * i;
+    const int row = min(c / (BK / 8), valid - 1);
+    const int piece = c % (BK / 8);
+    int64_t src_row;
+    if constexpr (GATEUP) src_row = perm[m0 + row] / top_k;
+    else src_row = m0 + row;
+    a_ptr[i] = A_src + src_row * (int64_t)Kdim + piece * 8;
+  }
+  const uint8_t* b_row[CH_B];
+#pragma unroll
+  for (int i = 0; i < CH_B; ++i) {
+    const int c = tid + NTHREADS * i;
+    const int j = c / (BK / 16);
+    int64_t wr;
+    if constexpr (GATEUP) {
+      const int half = BNW / 2;
+      const int n0 = nt * half;
+      wr = j < half ? (n0 + j) : (NI + n0 + (j - half));
+    } else {
+      wr = (int64_t)nt * BNW + j;
+    }
+    b_row[i] = wexp + wr * rb;
+  }
+
+  f32x16_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  u32x4_t areg[CH_A];
+  uint32_t breg[CH_B][8];
+  const int nk = Kdim / BK;
+
+  auto load_stage = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < CH_A; ++i) areg[i] = *(const u32x4_t*)(a_ptr[i] + k0);
+#pragma unroll
+    for (int i = 0; i < CH_B; ++i) {
+      const int c = tid + NTHREADS * i;
+      const int q = c % (BK / 16);
+      float y[16];
+      decode16<TYPE>(b_row[i], k0 + 16 * q, grid_lds, y);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) breg[i][k] = f2bf2(y[2 * k], y[2 * k + 1]);
+    }
+  };
+
+  if constexpr (TYPE == GGML_IQ3_S) __syncthreads();
+  load_stage(0);
+  for (int ks = 0; ks < nk; ++ks) {
+    __syncthreads();  // previous tile's MFMA reads are done
+#pragma unroll
+    for (int i = 0; i < CH_A; ++i) {
+      const int c = tid + NTHREADS * i;
+      const int row = c / (BK / 8), piece = c % (BK / 8);
+      *(u32x4_t*)(As + row * PITCH + piece * 8) = areg[i];
+    }
+#pragma unroll
+    for (int i = 0; i < CH_B; ++i) {
+      const int c = tid + NTHREADS * i;
+      const int j = c / (BK / 16), q = c % (BK / 16);
+      u32x4_t v0 = {breg[i][0], breg[i][1], breg[i][2], breg[i][3]};
+      u32x4_t v1 = {breg[i][4], breg[i][5], breg[i][6], breg[i][7]};
+      *(u32x4_t*)(Bs + j * PITCH + q * 16) = v0;
+      *(u32x4_t*)(Bs + j * PITCH + q * 16 + 8) = v1;
+    }
+    __syncthreads();
+    if (ks + 1 < nk) load_stage((ks + 1) * BK);
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 16) {
+      bf16x8_t af[FM], bfr[FN];
+      const int kof = kk + 8 * (lane >> 5);
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int row = wm * FM * 32 + i * 32 + (lane & 31);
+        af[i] = *(const bf16x8_t*)(As + row * PITCH + kof);
+      }
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        int brow;
+        if constexpr (GATEUP) {
+          brow = (j < FN / 2) ? (wn * (FN / 2) * 32 + j * 32) : (BNW / 2 + wn * (FN / 2) * 32 + (j - FN / 2) * 32);
+        } else {
+          brow = wn * FN * 32 + j * 32;
+        }
+        bfr[j] = *(const bf16x8_t*)(Bs + (brow + (lane & 31)) * PITCH + kof);
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // ---- epilogue. 32x32 accumulator layout: lane l, element r -> column l%32,
+  // row 8*(r/4) + 4*(l/32) + r%4.
+  const int col = lane & 31;
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int ml = wm * FM * 32 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      if (ml >= valid) continue;
+      if constexpr (GATEUP) {
+        const int n0 = nt * (BNW / 2);
+#pragma unroll
+        for (int j = 0; j < FN / 2; ++j) {
+          const float h = silu_mul(acc[i][j][r], acc[i][j + FN / 2][r]);
+          out[(int64_t)(m0 + ml) * NI + n0 + wn * (FN / 2) * 32 + j * 32 + col] = f2bf(h);
+        }
+      } else {
+        const int64_t p = perm[m0 + ml];
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          out[p * NI + (int64_t)nt * BNW + wn * FN * 32 + j * 32 + col] = f2bf(acc[i][j][r]);
+      }
+    }
+  }
+}
+
+// res[t, c] = bf16( sum_{k asc, slot_ids >= 0} fp32( bf16( Y[p, c] * bf16(w[p]) ) ) )
+__global__ __launch_bounds__(256) void combine_routes(const uint16_t* __restrict__ Y, const float* __restrict__ w,
+                                                      const int32_t* __restrict__ slot_ids, int S, int top_k,
+                                                      int64_t K, uint16_t* __restrict__ res) {
+  const int64_t t = blockIdx.y;
+  const int64_t c = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 2;
+  if (c >= K) return;
+  float a0 = 0.0f, a1 = 0.0f;
+  for (int k = 0; k < top_k; ++k) {
+    const int64_t p = t * top_k + k;
+    const int e = slot_ids[p];
+    if (e < 0 || e >= S) continue;
+    const float wk = bf2f(f2bf(w[p]));
+    const uint32_t v = *(const uint32_t*)(Y + p * K + c);
+    a0 += bf2f(f2bf(bf2f(v & 0xFFFF) * wk));
+    a1 += bf2f(f2bf(bf2f(v >> 16) * wk));
+  }
+  *(uint32_t*)(res + t * K + c) = f2bf2(a0, a1);
+}
+
+template <int TYPE, bool GATEUP>
+void launch_gemm(dim3 grid, hipStream_t stream, const uint16_t* A_src, const int32_t* perm, const int32_t* seg,
+                 const int32_t* tseg, int S, int top_k, const void* W, int w_is_table, int64_t w_expert_stride,
+                 int64_t rb, int Kdim, int NI, int NT, int64_t nblk, uint16_t* out) {
+  grouped_gemm<TYPE, GATEUP><<<grid, NTHREADS, 0, stream>>>(A_src, perm, seg, tseg, S, top_k, (const uint8_t*)W,
+                                                             w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out);
+}
+
+template <bool GATEUP>
+int dispatch_gemm(int type, dim3 grid, hipStream_t stream, const uint16_t* A_src, const int32_t* perm,
+                  const int32_t* seg, const int32_t* tseg, int S, int top_k, const void* W, int w_is_table,
+                  int64_t w_expert_stride, int64_t rb, int Kdim, int NI, int NT, int64_t nblk, uint16_t* out) {
+  switch (type) {
+    case GGML_Q8_0: launch_gemm<GGML_Q8_0, GATEUP>(grid, stream, A_src, perm, seg, tseg, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
+    case GGML_Q4_K: launch_gemm<GGML_Q4_K, GATEUP>(grid, stream, A_src, perm, seg, tseg, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
+    case GGML_Q6_K: launch_gemm<GGML_Q6_K, GATEUP>(grid, stream, A_src, perm, seg, tseg, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
+    case GGML_IQ3_S: launch_gemm<GGML_IQ3_S, GATEUP>(grid, stream, A_src, perm, seg, tseg, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
+    default: set_error("grouped GEMM: ggml type %d has no kernel", type); return KTMI_ETYPE;
+  }
+  KTMI_HIP_TRY(hipGetLastError());
+  return KTMI_OK;
+}
+
+inline int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
+
+}  // namespace
+
+GroupedPlan grouped_plan(int64_t tokens, int64_t top_k, int64_t n_slots, int64_t hidden, int64_t inter) {
+  GroupedPlan P{};
+  P.routes = tokens * top_k;
+  P.n_slots = n_slots;
+  const int64_t nch = (P.routes + CHW - 1) / CHW;
+  P.max_tiles = (P.routes + BM - 1) / BM + n_slots;
+  int64_t o = 0;
+  P.off_counts = o; o = align256(o + (nch > 0 ? nch : 1) * n_slots * 4);
+  P.off_seg = o; o = align256(o + (n_slots + 1) * 4);
+  P.off_tseg = o; o = align256(o + (n_slots + 1) * 4);
+  P.off_perm = o; o = align256(o + P.routes * 4);
+  P.off_h = o; o = align256(o + P.routes * inter * 2);
+  P.off_y = o; o = align256(o + P.routes * hidden * 2);
+  P.total = o;
+  return P;
+}
+
+int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* topk_w, const int32_t* slot_ids,
+                         int64_t tokens, int64_t top_k, uint16_t* y, uint8_t* ws, const GroupedPlan& P,
+                         hipStream_t stream) {
+  const int64_t R = P.routes;
+  const int S = (int)L->n_slots;
+  const int64_t K = L->hidden, N = L->inter;
+  KTMI_REQUIRE(S >= 1 && S <= MAX_SLOTS, KTMI_EINVAL, "grouped layer: n_slots %d outside [1, %d]", S, MAX_SLOTS);
+  KTMI_REQUIRE(K % BNW == 0 && K % BK == 0, KTMI_EINVAL, "grouped layer: hidden %lld not a multiple of %d",
+               (long long)K, BNW);
+  KTMI_REQUIRE(N % (BNW / 2) == 0 && N % BK == 0, KTMI_EINVAL,
+               "grouped layer: intermediate %lld not a multiple of %d", (long long)N, BNW / 2);
+  if (tokens == 0) return KTMI_OK;
+  int32_t* hist = (int32_t*)(ws + P.off_counts);
+  int32_t* seg = (int32_t*)(ws + P.off_seg);
+  int32_t* tseg = (int32_t*)(ws + P.off_tseg);
+  int32_t* perm = (int32_t*)(ws + P.off_perm);
+  uint16_t* H = (uint16_t*)(ws + P.off_h);
+  uint16_t* Y = (uint16_t*)(ws + P.off_y);
+  const int64_t nch = (R + CHW - 1) / CHW;
+  const unsigned sblocks = (unsigned)((nch + 3) / 4);
+  record_stage(0, stream);
+  sort_count<<<sblocks, SORT_THREADS, 0, stream>>>(slot_ids, R, S, hist, nch);
+  sort_scan<<<1, SORT_THREADS, 0, stream>>>(hist, nch, S, seg, tseg, BM);
+  sort_scatter<<<sblocks, SORT_THREADS, 0, stream>>>(slot_ids, R, S, hist, nch, seg, perm);
+  KTMI_HIP_TRY(hipGetLastError());
+
+  record_stage(1, stream);
+  const int64_t rb13 = row_bytes(K, L->type13), rb2 = row_bytes(N, L->type2);
+  const int64_t st13 = 2 * N * rb13, st2 = K * rb2;
+  const int NT1 = (int)(N / (BNW / 2));
+  const int64_t nblk1 = P.max_tiles * NT1;
+  dim3 g1((unsigned)((nblk1 + 8 * NT1 - 1) / (8 * NT1) * (8 * NT1)));
+  int rc = dispatch_gemm<true>(L->type13, g1, stream, x, perm, seg, tseg, S, (int)top_k, L->w13, L->w_is_table,
+                               st13, rb13, (int)K, (int)N, NT1, nblk1, H);
+  if (rc) return rc;
+  record_stage(2, stream);  // no mid stage on this path: SiLU*mul is in the gate/up epilogue
+  record_stage(3, stream);
+  const int NT2 = (int)(K / BNW);
+  const int64_t nblk2 = P.max_tiles * NT2;
+  dim3 g2((unsigned)((nblk2 + 8 * NT2 - 1) / (8 * NT2) * (8 * NT2)));
+  rc = dispatch_gemm<false>(L->type2, g2, stream, H, perm, seg, tseg, S, (int)top_k, L->w2, L->w_is_table, st2, rb2,
+                            (int)N, (int)K, NT2, nblk2, Y);
+  if (rc) return rc;
+  record_stage(4, stream);
+  for (int64_t t0 = 0; t0 < tokens; t0 += 65535) {
+    const int64_t nt = tokens - t0 < 65535 ? tokens - t0 : 65535;
+    dim3 gc((unsigned)((K / 2 + 255) / 256), (unsigned)nt);
+    combine_routes<<<gc, 256, 0, stream>>>(Y + t0 * top_k * K, topk_w + t0 * top_k, slot_ids + t0 * top_k, S,
+                                           (int)top_k, K, y + t0 * K);
+  }
+  record_stage(5, stream);
+  KTMI_HIP_TRY(hipGetLastError());
+  return KTMI_OK;
+}
+
+}  // namespace ktmi

@@ -1,0 +1,42 @@
+"""Shared input builders for the tests (seeded, small)."""
+import numpy as np
+
+from oracle import gguf_ref as R
+
+TYPES = [R.GGML_Q8_0, R.GGML_Q4_K, R.GGML_Q6_K, R.GGML_IQ3_S]
+# byte offsets of the fp16 fields inside one block
+_F16_FIELDS = {R.GGML_Q8_0: (0,), R.GGML_Q4_K: (0, 2), R.GGML_Q6_K: (208,), R.GGML_IQ3_S: (0,)}
+
+
+def random_blocks(t: int, rows: int, cols: int, rng: np.random.Generator) -> np.ndarray:
+    """uint8 [rows, row_bytes]: uniformly random bytes (every code, sign, grid index and
+    scale pattern) with the fp16 scale fields set to finite values of mixed sign."""
+    blck, ts = R.BLOCK_INFO[t]
+    nb = cols // blck
+    b = rng.integers(0, 256, size=(rows, nb, ts), dtype=np.uint8)
+    for off in _F16_FIELDS[t]:
+        mag = rng.uniform(1e-4, 0.05, size=(rows, nb)).astype(np.float32)
+        sign = np.where(rng.random((rows, nb)) < 0.2, -1.0, 1.0).astype(np.float32)
+        h = (mag * sign).astype(np.float16).view(np.uint8).reshape(rows, nb, 2)
+        b[:, :, off:off + 2] = h
+    return b.reshape(rows, nb * ts)
+
+
+def dequant_w(w13: np.ndarray, w2: np.ndarray, types, hidden: int, inter: int):
+    """bf16-rounded fp32 weights of the slot tensors: [S, 2N, K], [S, K, N]."""
+    S = w13.shape[0]
+    g = R.bf16_round(R.dequant_rows(w13.reshape(S * 2 * inter, -1), types[0], hidden)).reshape(S, 2 * inter, hidden)
+    d = R.bf16_round(R.dequant_rows(w2.reshape(S * hidden, -1), types[2], inter)).reshape(S, hidden, inter)
+    return g, d
+
+
+def gemv_layer_oracle(x_bits, topk_w, slot_ids, w13, w2, types, hidden, inter):
+    """The decode path's own numerics, step by step in the oracle: q8_1(x) GEMV -> bf16,
+    SiLU*mul -> bf16, q8_1(h) GEMV -> bf16, combine."""
+    T, k = slot_ids.shape
+    ids = slot_ids.reshape(-1)
+    x = R.bf16_to_f32(x_bits)
+    h13 = R.bf16_bits(R.moe_a8_vec(x, w13, ids, k, types[0], 2 * inter, T).astype(np.float32))
+    h = R.silu_and_mul(h13)
+    out = R.bf16_bits(R.moe_a8_vec(R.bf16_to_f32(h), w2, ids, 1, types[2], hidden, T * k).astype(np.float32))
+    return R.combine(out.reshape(T, k, hidden), topk_w)

@@ -1,0 +1,121 @@
+"""GPU parity of the whole hot-expert layer (GEMV and grouped MFMA modes) against the
+oracle's `_reference_check` FFN, through the C ABI."""
+from dataclasses import replace
+
+import numpy as np
+import pytest
+
+from conftest import bf16_bits_of, bf16_tensor, to_dev
+from helpers import dequant_w, gemv_layer_oracle
+from oracle import gguf_ref as R
+
+pytestmark = pytest.mark.gpu
+
+TOL_REL_L2 = 2e-2  # layer outputs vs the fp64 FFN on the bf16-dequantised weights
+
+
+def _pkg():
+    import kt_prefill_lend_amd._lib as L
+    import kt_prefill_lend_amd.kt_gguf_hot as H
+    import kt_prefill_lend_amd.synth as S
+
+    return L, H, S
+
+
+def _case(name, tokens, hidden=None, inter=None, hot=None, experts=None):
+    _, _, S = _pkg()
+    w = S.WORKLOADS[name]
+    w = replace(w, hidden=hidden or w.hidden, inter=inter or w.inter, hot=hot or w.hot, experts=experts or w.experts)
+    ids, tw, slot, _ = S.routing(w, tokens)
+    xb = S.activations(w, tokens)
+    w13, w2 = S.slot_tensors(w)
+    return w, xb, tw, slot, w13, w2
+
+
+def _run(dev, w, xb, tw, slot, w13, w2, mode):
+    import torch
+
+    L, H, _ = _pkg()
+    W13, W2 = to_dev(w13, dev), to_dev(w2, dev)
+    desc = H.layer_desc(W13, W2, w.hidden, w.inter, w.types[0], w.types[2])
+    y = H.moe_layer(desc, bf16_tensor(xb, dev), to_dev(tw, dev), to_dev(slot, dev), mode)
+    torch.cuda.synchronize()
+    return bf16_bits_of(y)
+
+
+CASES = [
+    # (workload, tokens, hidden, inter, hot, experts)
+    ("q8_0-h2048-n768-e128-k8-hot16", 40, 512, 256, 6, 24),
+    ("q4_k-h2048-n512-e256-k8-hot32-decode", 16, 512, 256, 8, 32),
+    ("q4_k+q6_k-h2048-n512-e256-k8-hot40-prefill", 48, 512, 256, 8, 32),
+    ("iq3_s-h2048-n512-e512-k10-hot48", 40, 512, 256, 8, 40),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0].split("-")[0] for c in CASES])
+@pytest.mark.parametrize("mode", ["gemv", "grouped"])
+def test_layer_vs_ffn_reference(dev, case, mode):
+    L, _, _ = _pkg()
+    w, xb, tw, slot, w13, w2 = _case(*case)
+    m = L.MODE_GEMV if mode == "gemv" else L.MODE_GROUPED
+    got = R.bf16_to_f32(_run(dev, w, xb, tw, slot, w13, w2, m))
+    g, d = dequant_w(w13, w2, w.types, w.hidden, w.inter)
+    ref = R.ffn_reference(xb, slot, tw, g, d)
+    l2, l1, cos = R.rel_errors(got, ref)
+    print(f"{case[0]} {mode}: rel L2 {l2:.2e} rel L1 {l1:.2e} cos {cos:.6f}")
+    assert l2 < TOL_REL_L2 and l1 < 0.025 and cos > 0.999, (l2, l1, cos)
+    # tokens with no hot route are exactly zero
+    cold_tok = (slot < 0).all(axis=1)
+    assert np.all(got[cold_tok] == 0)
+
+
+def test_gemv_mode_matches_reference_kernel_numerics(dev):
+    """The decode path reproduces the reference kernels' own sequence (q8_1 GEMV, bf16,
+    SiLU*mul, q8_1 GEMV, combine) to bf16 rounding."""
+    L, _, _ = _pkg()
+    w, xb, tw, slot, w13, w2 = _case("q4_k-h2048-n512-e256-k8-hot32-decode", 4, 512, 256, 8, 32)
+    got = R.bf16_to_f32(_run(dev, w, xb, tw, slot, w13, w2, L.MODE_GEMV))
+    exp = R.bf16_to_f32(gemv_layer_oracle(xb, tw, slot, w13, w2, w.types, w.hidden, w.inter))
+    l2, _, _ = R.rel_errors(got, exp)
+    assert l2 < 4e-3, l2
+
+
+@pytest.mark.parametrize("mode", ["gemv", "grouped"])
+def test_layer_deterministic(dev, mode):
+    L, _, _ = _pkg()
+    w, xb, tw, slot, w13, w2 = _case("q4_k+q6_k-h2048-n512-e256-k8-hot40-prefill", 300, 512, 256, 8, 32)
+    m = L.MODE_GEMV if mode == "gemv" else L.MODE_GROUPED
+    a = _run(dev, w, xb, tw, slot, w13, w2, m)
+    b = _run(dev, w, xb, tw, slot, w13, w2, m)
+    assert np.array_equal(a, b)
+
+
+def test_grouped_edge_cases(dev):
+    """Empty slots, a single token, all-cold tokens, slots with one route."""
+    L, _, _ = _pkg()
+    w, xb, tw, slot, w13, w2 = _case("q4_k+q6_k-h2048-n512-e256-k8-hot40-prefill", 5, 512, 256, 8, 32)
+    slot = slot.copy()
+    slot[0, :] = -1          # a token with no hot route
+    slot[1, :] = -1
+    slot[1, 3] = 7           # slot 7 with exactly one route
+    for T in (1, 5):
+        got = R.bf16_to_f32(_run(dev, w, xb[:T], tw[:T], slot[:T], w13, w2, L.MODE_GROUPED))
+        g, d = dequant_w(w13, w2, w.types, w.hidden, w.inter)
+        ref = R.ffn_reference(xb[:T], slot[:T], tw[:T], g, d)
+        assert np.all(got[0] == 0)
+        if T > 1:
+            l2, _, _ = R.rel_errors(got, ref)
+            assert l2 < TOL_REL_L2
+
+
+def test_grouped_at_full_shape(dev):
+    """The prefill workload's real layer shape (hidden 2048, inter 512, 40 slots, Q4_K/Q6_K)
+    at 1024 tokens, against the fp64 FFN on a sample of tokens."""
+    L, _, _ = _pkg()
+    w, xb, tw, slot, w13, w2 = _case("q4_k+q6_k-h2048-n512-e256-k8-hot40-prefill", 1024)
+    got = R.bf16_to_f32(_run(dev, w, xb, tw, slot, w13, w2, L.MODE_GROUPED))
+    g, d = dequant_w(w13, w2, w.types, w.hidden, w.inter)
+    sample = np.arange(0, 1024, 8)
+    ref = R.ffn_reference(xb[sample], slot[sample], tw[sample], g, d)
+    l2, l1, cos = R.rel_errors(got[sample], ref)
+    assert l2 < TOL_REL_L2 and cos > 0.999, (l2, l1, cos)
