@@ -18,24 +18,38 @@
 // Reference: the streamer's per-group dequant + cutlass_fused_moe + acc.add_ (P:40789-40819,
 // dequant P:11471-11498), _combine (hot/kt_gguf_hot.py:43-71); the sort-by-expert follows the
 // idea of moe_prepare_ids_kernel (P:31142-31162) with a deterministic stable order.
-#include "formats.h"
+#include "bpiece.h"
 #include "kernels.h"
 
 namespace ktmi {
 
 namespace {
 
-constexpr int CHW = 1024;        // routes per wave chunk in the sort
+constexpr int CHW = 256;         // routes per wave chunk in the sort
 constexpr int SORT_THREADS = 256;
 constexpr int MAX_SLOTS = 512;
 
-// tile configuration
+// tile configuration: 8 waves in 2 (M) x 4 (N), each 128 routes x 64 weight rows;
+// tile = 256 routes x 256 weight rows (GATEUP: 128 gate + 128 up rows)
 constexpr int BK = 64;
-constexpr int PITCH = BK + 8;  // bf16 elements per LDS row (16-byte pad against bank conflicts)
-constexpr int FM = 2, FN = 2, WM = 2, WN = 2;
+constexpr int FM = 4, FN = 2, WM = 2, WN = 4;
 constexpr int NTHREADS = WM * WN * 64;
+constexpr int NWAVES = WM * WN;
 constexpr int BM = WM * FM * 32;   // routes per tile
-constexpr int BNW = WN * FN * 32;  // weight rows per tile (gate+up for GATEUP)
+constexpr int BNW = WN * FN * 32;  // weight rows per tile
+// LDS: A tile double-buffered, 128 B per row (8 swizzled 16-byte slots, no pad), written
+// by direct global->LDS loads; B tile double-buffered, padded rows written by ds_write.
+constexpr int A_BYTES = BM * BK * 2;
+constexpr int BPITCH = BK + 8;  // bf16 elements per B row
+constexpr int B_BYTES = BNW * BPITCH * 2;
+constexpr int SMEM_AB = 2 * A_BYTES + 2 * B_BYTES;
+constexpr int CPITCH_UP = BNW / 2 + 8;  // epilogue C tile pitches (bf16 elements)
+constexpr int CPITCH_DN = BNW + 8;
+constexpr int SMEM_C = BM * CPITCH_DN * 2;
+constexpr int SMEM = SMEM_AB > SMEM_C ? SMEM_AB : SMEM_C;
+static_assert(SMEM <= 160 * 1024, "LDS");
+
+// ---- route sort by slot. hist is slot-major: hist[e * nch + chunk].
 
 __global__ __launch_bounds__(SORT_THREADS) void sort_count(const int32_t* __restrict__ slot_ids, int64_t R, int S,
                                                            int32_t* __restrict__ hist, int64_t nch) {
@@ -56,38 +70,63 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_count(const int32_t* __rest
   }
   __syncthreads();
   if (ch < nch)
-    for (int e = lane; e < S; e += 64) hist[ch * S + e] = cnt[w][e];
+    for (int e = lane; e < S; e += 64) hist[(int64_t)e * nch + ch] = cnt[w][e];
 }
 
-// one workgroup: per-slot exclusive prefix over chunks (in place), then slot offsets
-// seg[S+1] and tile offsets tseg[S+1] (tiles of BM routes)
-__global__ __launch_bounds__(SORT_THREADS) void sort_scan(int32_t* __restrict__ hist, int64_t nch, int S,
-                                                          int32_t* __restrict__ seg, int32_t* __restrict__ tseg,
-                                                          int bm) {
-  __shared__ int tot[MAX_SLOTS];
-  __shared__ int til[MAX_SLOTS];
-  for (int e = threadIdx.x; e < S; e += blockDim.x) {
-    int run = 0;
-    for (int64_t c = 0; c < nch; ++c) {
-      const int v = hist[c * S + e];
-      hist[c * S + e] = run;
-      run += v;
-    }
-    tot[e] = run;
-    til[e] = (run + bm - 1) / bm;
-  }
+// exclusive block scan of 256 ints in LDS (returns the total)
+__device__ int block_scan_256(int* buf, int v) {
+  const int t = threadIdx.x;
+  buf[t] = v;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int a = 0, b = 0;
-    for (int e = 0; e < S; ++e) {
-      seg[e] = a;
-      tseg[e] = b;
-      a += tot[e];
-      b += til[e];
-    }
-    seg[S] = a;
-    tseg[S] = b;
+  for (int off = 1; off < 256; off <<= 1) {
+    const int a = t >= off ? buf[t - off] : 0;
+    __syncthreads();
+    buf[t] += a;
+    __syncthreads();
   }
+  const int incl = buf[t];
+  const int total = buf[255];
+  __syncthreads();
+  buf[t] = incl - v;
+  return total;
+}
+
+// grid S: block e turns hist[e, :] into its exclusive prefix over chunks; tot[e] = total
+__global__ __launch_bounds__(SORT_THREADS) void sort_scan_chunks(int32_t* __restrict__ hist, int64_t nch,
+                                                                 int32_t* __restrict__ tot) {
+  __shared__ int buf[SORT_THREADS];
+  int32_t* h = hist + (int64_t)blockIdx.x * nch;
+  const int64_t per = (nch + SORT_THREADS - 1) / SORT_THREADS;
+  const int64_t c0 = threadIdx.x * per;
+  int sum = 0;
+  for (int64_t c = c0; c < c0 + per && c < nch; ++c) sum += h[c];
+  const int total = block_scan_256(buf, sum);
+  int run = buf[threadIdx.x];
+  for (int64_t c = c0; c < c0 + per && c < nch; ++c) {
+    const int v = h[c];
+    h[c] = run;
+    run += v;
+  }
+  if (threadIdx.x == 0) tot[blockIdx.x] = total;
+}
+
+// one block: seg[S+1] (route offsets) and tseg[S+1] (tile offsets, tiles of bm routes)
+__global__ __launch_bounds__(SORT_THREADS) void sort_scan_slots(const int32_t* __restrict__ tot, int S,
+                                                                int32_t* __restrict__ seg,
+                                                                int32_t* __restrict__ tseg, int bm) {
+  __shared__ int buf[SORT_THREADS];
+  const int t = threadIdx.x;
+  // two slots per thread (S <= 512)
+  const int e0 = 2 * t, e1 = 2 * t + 1;
+  const int a0 = e0 < S ? tot[e0] : 0, a1 = e1 < S ? tot[e1] : 0;
+  const int b0 = (a0 + bm - 1) / bm, b1 = (a1 + bm - 1) / bm;
+  const int ta = block_scan_256(buf, a0 + a1);
+  const int ea = buf[t];
+  const int tb = block_scan_256(buf, b0 + b1);
+  const int eb = buf[t];
+  if (e0 < S) { seg[e0] = ea; tseg[e0] = eb; }
+  if (e1 < S) { seg[e1] = ea + a0; tseg[e1] = eb + b0; }
+  if (t == 0) { seg[S] = ta; tseg[S] = tb; }
 }
 
 __global__ __launch_bounds__(SORT_THREADS) void sort_scatter(const int32_t* __restrict__ slot_ids, int64_t R, int S,
@@ -98,8 +137,7 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_scatter(const int32_t* __re
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t ch = (int64_t)blockIdx.x * (SORT_THREADS / 64) + w;
   if (ch >= nch) return;  // whole wave; no block-wide barrier below
-  for (int e = lane; e < S; e += 64) run[w][e] = seg[e] + hist[ch * S + e];
-  __builtin_amdgcn_s_waitcnt(0);
+  for (int e = lane; e < S; e += 64) run[w][e] = seg[e] + hist[(int64_t)e * nch + ch];
   __builtin_amdgcn_wave_barrier();
   const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   const int64_t p0 = ch * CHW;
@@ -127,7 +165,6 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_scatter(const int32_t* __re
       perm[base + rank] = (int32_t)p;
       if ((same & lt) == 0) run[w][e] = base + __popcll(same);  // lowest lane of the group
     }
-    __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_wave_barrier();
   }
 }
@@ -138,6 +175,15 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f +
 //                 B rows = [gate n0..n0+BNW/2 ; up NI+n0..], out = H [R, NI] sorted rows.
 // GATEUP = false: A = H rows m0.., Kdim = inter, B rows = down rows c0..c0+BNW,
 //                 out = Y [routes, NI] at row perm[m] (NI = hidden).
+//
+// K loop, one barrier per 64-value step k:
+//   issue A(k+1) global->LDS into Abuf[(k+1)&1], issue the raw B bytes of step k+1;
+//   MFMAs of step k from Abuf[k&1], Bbuf[k&1];
+//   decode B(k+1) (bpiece.h) into Bbuf[(k+1)&1]; wait for the loads; barrier.
+// A rows are 128 B in LDS, 16-byte slot = chunk ^ ((row >> 1) & 7): the 16 lanes of one
+// ds_read_b128 pass (rows r..r+15) then hit 16 different slot/bank groups.
+__device__ __forceinline__ int a_slot(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+
 template <int TYPE, bool GATEUP>
 __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restrict__ A_src,
                                                          const int32_t* __restrict__ perm,
@@ -146,9 +192,9 @@ __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restr
                                                          const uint8_t* __restrict__ W, int w_is_table,
                                                          int64_t w_expert_stride, int64_t rb, int Kdim, int NI,
                                                          int NT, int64_t nblk, uint16_t* __restrict__ out) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[BM * PITCH];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[BNW * PITCH];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
   __shared__ uint32_t grid_lds[TYPE == GGML_IQ3_S ? 512 : 1];
+  using BP = BPiece<TYPE>;
 
   // XCD-aware order: workgroups are dealt to the 8 XCDs round-robin (pid % 8). All NT
   // N tiles of one M tile go to the same XCD, so they share its L2 for the gathered A
@@ -176,36 +222,53 @@ __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restr
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const uint8_t* wexp = w_is_table ? (const uint8_t*)((const int64_t*)W)[e] : W + (int64_t)e * w_expert_stride;
+  uint8_t* Abuf0 = smem;
+  uint8_t* Bbuf0 = smem + 2 * A_BYTES;
 
-  // ---- per-thread global sources (fixed over the K loop)
-  constexpr int CH_A = BM * (BK / 8) / NTHREADS;   // 16-byte pieces of A per thread
-  constexpr int CH_B = BNW * (BK / 16) / NTHREADS; // 16-value pieces of B per thread
-  const uint16_t* a_ptr[CH_A];
+  // ---- A sources: direct loads, instruction j of wave w fills rows 8*(NWAVES*j + w) + lane/8
+  constexpr int AJ = BM / (8 * NWAVES);
+  int a_off[AJ];  // element offset of this lane's 16-byte chunk (without k0)
 #pragma unroll
-  for (int i = 0; i < CH_A; ++i) {
-    const int c = tid + NTHREADS * i;
-    const int row = min(c / (BK / 8), valid - 1);
-    const int piece = c % (BK / 8);
-    int64_t src_row;
-    if constexpr (GATEUP) src_row = perm[m0 + row] / top_k;
-    else src_row = m0 + row;
-    a_ptr[i] = A_src + src_row * (int64_t)Kdim + piece * 8;
+  for (int j = 0; j < AJ; ++j) {
+    const int row = 8 * (NWAVES * j + wave) + (lane >> 3);
+    const int chunk = (lane & 7) ^ ((row >> 1) & 7);
+    const int r = min(row, valid - 1);
+    int src_row;
+    if constexpr (GATEUP) src_row = perm[m0 + r] / top_k;
+    else src_row = m0 + r;
+    a_off[j] = src_row * Kdim + 8 * chunk;
   }
-  const uint8_t* b_row[CH_B];
+  auto issue_a = [&](int k0, int buf) {
 #pragma unroll
-  for (int i = 0; i < CH_B; ++i) {
-    const int c = tid + NTHREADS * i;
-    const int j = c / (BK / 16);
-    int64_t wr;
-    if constexpr (GATEUP) {
-      const int half = BNW / 2;
-      const int n0 = nt * half;
-      wr = j < half ? (n0 + j) : (NI + n0 + (j - half));
-    } else {
-      wr = (int64_t)nt * BNW + j;
+    for (int j = 0; j < AJ; ++j) {
+      uint8_t* dst = Abuf0 + buf * A_BYTES + (8 * (NWAVES * j + wave)) * (BK * 2);
+      __builtin_amdgcn_global_load_lds(A_src + a_off[j] + k0, dst, 16, 0, 0);
     }
-    b_row[i] = wexp + wr * rb;
+  };
+
+  // ---- B source: one 32-value piece per thread (row bj, half bh of the K step)
+  static_assert(BNW * 2 == NTHREADS, "one 32-value B piece per thread");
+  const int bj = tid >> 1, bh = tid & 1;
+  int64_t wr;
+  if constexpr (GATEUP) {
+    const int half = BNW / 2;
+    const int n0 = nt * half;
+    wr = bj < half ? (n0 + bj) : (NI + n0 + (bj - half));
+  } else {
+    wr = (int64_t)nt * BNW + bj;
   }
+  const uint8_t* b_row = wexp + wr * rb;
+  auto store_b = [&](const uint32_t* breg, int buf) {
+    uint16_t* bd = (uint16_t*)(Bbuf0 + buf * B_BYTES) + bj * BPITCH;
+    u32x4_t v0 = {breg[0], breg[1], breg[2], breg[3]};
+    u32x4_t v1 = {breg[4], breg[5], breg[6], breg[7]};
+    u32x4_t v2 = {breg[8], breg[9], breg[10], breg[11]};
+    u32x4_t v3 = {breg[12], breg[13], breg[14], breg[15]};
+    *(u32x4_t*)(bd + BP::off0(bh)) = v0;
+    *(u32x4_t*)(bd + BP::off0(bh) + 8) = v1;
+    *(u32x4_t*)(bd + BP::off1(bh)) = v2;
+    *(u32x4_t*)(bd + BP::off1(bh) + 8) = v3;
+  };
 
   f32x16_t acc[FM][FN];
 #pragma unroll
@@ -215,54 +278,37 @@ __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restr
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  u32x4_t areg[CH_A];
-  uint32_t breg[CH_B][8];
+  typename BP::Raw braw;
+  uint32_t breg[16];
   const int nk = Kdim / BK;
 
-  auto load_stage = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < CH_A; ++i) areg[i] = *(const u32x4_t*)(a_ptr[i] + k0);
-#pragma unroll
-    for (int i = 0; i < CH_B; ++i) {
-      const int c = tid + NTHREADS * i;
-      const int q = c % (BK / 16);
-      float y[16];
-      decode16<TYPE>(b_row[i], k0 + 16 * q, grid_lds, y);
-#pragma unroll
-      for (int k = 0; k < 8; ++k) breg[i][k] = f2bf2(y[2 * k], y[2 * k + 1]);
-    }
-  };
-
   if constexpr (TYPE == GGML_IQ3_S) __syncthreads();
-  load_stage(0);
+  issue_a(0, 0);
+  BP::load(b_row, 0, bh, grid_lds, braw);
+  BP::decode(braw, grid_lds, breg);
+  store_b(breg, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
   for (int ks = 0; ks < nk; ++ks) {
-    __syncthreads();  // previous tile's MFMA reads are done
-#pragma unroll
-    for (int i = 0; i < CH_A; ++i) {
-      const int c = tid + NTHREADS * i;
-      const int row = c / (BK / 8), piece = c % (BK / 8);
-      *(u32x4_t*)(As + row * PITCH + piece * 8) = areg[i];
+    const int buf = ks & 1;
+    const bool more = ks + 1 < nk;
+    if (more) {
+      issue_a((ks + 1) * BK, buf ^ 1);
+      BP::load(b_row, (ks + 1) * BK, bh, grid_lds, braw);
     }
-#pragma unroll
-    for (int i = 0; i < CH_B; ++i) {
-      const int c = tid + NTHREADS * i;
-      const int j = c / (BK / 16), q = c % (BK / 16);
-      u32x4_t v0 = {breg[i][0], breg[i][1], breg[i][2], breg[i][3]};
-      u32x4_t v1 = {breg[i][4], breg[i][5], breg[i][6], breg[i][7]};
-      *(u32x4_t*)(Bs + j * PITCH + q * 16) = v0;
-      *(u32x4_t*)(Bs + j * PITCH + q * 16 + 8) = v1;
-    }
-    __syncthreads();
-    if (ks + 1 < nk) load_stage((ks + 1) * BK);
+    const uint8_t* Ab = Abuf0 + buf * A_BYTES;
+    const uint16_t* Bb = (const uint16_t*)(Bbuf0 + buf * B_BYTES);
 #pragma unroll
     for (int kk = 0; kk < BK; kk += 16) {
       bf16x8_t af[FM], bfr[FN];
-      const int kof = kk + 8 * (lane >> 5);
+      const int chunk = (kk >> 3) + (lane >> 5);
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
         const int row = wm * FM * 32 + i * 32 + (lane & 31);
-        af[i] = *(const bf16x8_t*)(As + row * PITCH + kof);
+        af[i] = *(const bf16x8_t*)(Ab + row * (BK * 2) + a_slot(row, chunk) * 16);
       }
+      const int kof = kk + 8 * (lane >> 5);
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         int brow;
@@ -271,7 +317,7 @@ __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restr
         } else {
           brow = wn * FN * 32 + j * 32;
         }
-        bfr[j] = *(const bf16x8_t*)(Bs + (brow + (lane & 31)) * PITCH + kof);
+        bfr[j] = *(const bf16x8_t*)(Bb + (brow + (lane & 31)) * BPITCH + kof);
       }
 #pragma unroll
       for (int i = 0; i < FM; ++i)
@@ -279,52 +325,85 @@ __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restr
         for (int j = 0; j < FN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
     }
+    if (more) {
+      BP::decode(braw, grid_lds, breg);
+      store_b(breg, buf ^ 1);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's A(k+1) direct loads and B stores have landed
+    __syncthreads();
   }
 
-  // ---- epilogue. 32x32 accumulator layout: lane l, element r -> column l%32,
-  // row 8*(r/4) + 4*(l/32) + r%4.
+  // ---- epilogue through LDS. 32x32 accumulator layout: lane l, element r -> column l%32,
+  // row 8*(r/4) + 4*(l/32) + r%4. The C tile is staged as bf16 in LDS, then written out
+  // in 16-byte row chunks.
+  uint16_t* cs = (uint16_t*)smem;
   const int col = lane & 31;
+  if constexpr (GATEUP) {
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int ml = wm * FM * 32 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-      if (ml >= valid) continue;
-      if constexpr (GATEUP) {
-        const int n0 = nt * (BNW / 2);
+      for (int r = 0; r < 16; ++r) {
+        const int ml = wm * FM * 32 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
 #pragma unroll
-        for (int j = 0; j < FN / 2; ++j) {
-          const float h = silu_mul(acc[i][j][r], acc[i][j + FN / 2][r]);
-          out[(int64_t)(m0 + ml) * NI + n0 + wn * (FN / 2) * 32 + j * 32 + col] = f2bf(h);
-        }
-      } else {
+        for (int j = 0; j < FN / 2; ++j)
+          cs[ml * CPITCH_UP + wn * (FN / 2) * 32 + j * 32 + col] = f2bf(silu_mul(acc[i][j][r], acc[i][j + FN / 2][r]));
+      }
+    __syncthreads();
+    constexpr int CW = BNW / 2 / 8;  // 16-byte chunks per row
+    const int n0 = nt * (BNW / 2);
+    for (int c = tid; c < BM * CW; c += NTHREADS) {
+      const int ml = c / CW, q = c % CW;
+      if (ml < valid)
+        *(u32x4_t*)(out + (int64_t)(m0 + ml) * NI + n0 + 8 * q) = *(const u32x4_t*)(cs + ml * CPITCH_UP + 8 * q);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int ml = wm * FM * 32 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) cs[ml * CPITCH_DN + wn * FN * 32 + j * 32 + col] = f2bf(acc[i][j][r]);
+      }
+    __syncthreads();
+    constexpr int CW = BNW / 8;
+    for (int c = tid; c < BM * CW; c += NTHREADS) {
+      const int ml = c / CW, q = c % CW;
+      if (ml < valid) {
         const int64_t p = perm[m0 + ml];
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          out[p * NI + (int64_t)nt * BNW + wn * FN * 32 + j * 32 + col] = f2bf(acc[i][j][r]);
+        *(u32x4_t*)(out + p * NI + (int64_t)nt * BNW + 8 * q) = *(const u32x4_t*)(cs + ml * CPITCH_DN + 8 * q);
       }
     }
   }
 }
 
-// res[t, c] = bf16( sum_{k asc, slot_ids >= 0} fp32( bf16( Y[p, c] * bf16(w[p]) ) ) )
+// res[t, c] = bf16( sum_{k asc, slot_ids >= 0} fp32( bf16( Y[p, c] * bf16(w[p]) ) ) ), 8 columns
+// per thread
 __global__ __launch_bounds__(256) void combine_routes(const uint16_t* __restrict__ Y, const float* __restrict__ w,
                                                       const int32_t* __restrict__ slot_ids, int S, int top_k,
                                                       int64_t K, uint16_t* __restrict__ res) {
   const int64_t t = blockIdx.y;
-  const int64_t c = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 2;
-  if (c >= K) return;
-  float a0 = 0.0f, a1 = 0.0f;
-  for (int k = 0; k < top_k; ++k) {
-    const int64_t p = t * top_k + k;
-    const int e = slot_ids[p];
-    if (e < 0 || e >= S) continue;
-    const float wk = bf2f(f2bf(w[p]));
-    const uint32_t v = *(const uint32_t*)(Y + p * K + c);
-    a0 += bf2f(f2bf(bf2f(v & 0xFFFF) * wk));
-    a1 += bf2f(f2bf(bf2f(v >> 16) * wk));
+  for (int64_t c = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8; c < K; c += (int64_t)gridDim.x * blockDim.x * 8) {
+    float a[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[i] = 0.0f;
+    for (int k = 0; k < top_k; ++k) {
+      const int64_t p = t * top_k + k;
+      const int e = slot_ids[p];
+      if (e < 0 || e >= S) continue;
+      const float wk = bf2f(f2bf(w[p]));
+      const u32x4_t v = *(const u32x4_t*)(Y + p * K + c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a[2 * i] += bf2f(f2bf(bf2f(v[i] & 0xFFFF) * wk));
+        a[2 * i + 1] += bf2f(f2bf(bf2f(v[i] >> 16) * wk));
+      }
+    }
+    u32x4_t o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = f2bf2(a[2 * i], a[2 * i + 1]);
+    *(u32x4_t*)(res + t * K + c) = o;
   }
-  *(uint32_t*)(res + t * K + c) = f2bf2(a0, a1);
 }
 
 template <int TYPE, bool GATEUP>
@@ -361,7 +440,7 @@ GroupedPlan grouped_plan(int64_t tokens, int64_t top_k, int64_t n_slots, int64_t
   const int64_t nch = (P.routes + CHW - 1) / CHW;
   P.max_tiles = (P.routes + BM - 1) / BM + n_slots;
   int64_t o = 0;
-  P.off_counts = o; o = align256(o + (nch > 0 ? nch : 1) * n_slots * 4);
+  P.off_counts = o; o = align256(o + ((nch > 0 ? nch : 1) * n_slots + n_slots) * 4);
   P.off_seg = o; o = align256(o + (n_slots + 1) * 4);
   P.off_tseg = o; o = align256(o + (n_slots + 1) * 4);
   P.off_perm = o; o = align256(o + P.routes * 4);
@@ -390,13 +469,14 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
   uint16_t* H = (uint16_t*)(ws + P.off_h);
   uint16_t* Y = (uint16_t*)(ws + P.off_y);
   const int64_t nch = (R + CHW - 1) / CHW;
+  int32_t* tot = hist + nch * S;
   const unsigned sblocks = (unsigned)((nch + 3) / 4);
   record_stage(0, stream);
   sort_count<<<sblocks, SORT_THREADS, 0, stream>>>(slot_ids, R, S, hist, nch);
-  sort_scan<<<1, SORT_THREADS, 0, stream>>>(hist, nch, S, seg, tseg, BM);
+  sort_scan_chunks<<<S, SORT_THREADS, 0, stream>>>(hist, nch, tot);
+  sort_scan_slots<<<1, SORT_THREADS, 0, stream>>>(tot, S, seg, tseg, BM);
   sort_scatter<<<sblocks, SORT_THREADS, 0, stream>>>(slot_ids, R, S, hist, nch, seg, perm);
   KTMI_HIP_TRY(hipGetLastError());
-
   record_stage(1, stream);
   const int64_t rb13 = row_bytes(K, L->type13), rb2 = row_bytes(N, L->type2);
   const int64_t st13 = 2 * N * rb13, st2 = K * rb2;
@@ -417,7 +497,7 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
   record_stage(4, stream);
   for (int64_t t0 = 0; t0 < tokens; t0 += 65535) {
     const int64_t nt = tokens - t0 < 65535 ? tokens - t0 : 65535;
-    dim3 gc((unsigned)((K / 2 + 255) / 256), (unsigned)nt);
+    dim3 gc((unsigned)((K / 8 + 255) / 256), (unsigned)nt);
     combine_routes<<<gc, 256, 0, stream>>>(Y + t0 * top_k * K, topk_w + t0 * top_k, slot_ids + t0 * top_k, S,
                                            (int)top_k, K, y + t0 * K);
   }
