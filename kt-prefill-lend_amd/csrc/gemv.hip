@@ -90,9 +90,9 @@ struct Unit<GGML_Q4_K> {
   __device__ static void load(const uint8_t* row, int u, const uint32_t*, W& w) {
     const uint8_t* b = row + (int64_t)(u >> 2) * QB4_K;
     const int g = u & 3;
-    const u32x4_t h0 = *(const u32x4_t*)b;  // d, dmin, scales[12]
-    const u32x4_t v0 = *(const u32x4_t*)(b + 16 + 32 * g);
-    const u32x4_t v1 = *(const u32x4_t*)(b + 32 + 32 * g);
+    const u32x4_t h0 = gload<u32x4_t>(b);  // d, dmin, scales[12]
+    const u32x4_t v0 = gload<u32x4_t>(b + 16 + 32 * g);
+    const u32x4_t v1 = gload<u32x4_t>(b + 32 + 32 * g);
     w.d = half_bits_to_float(h0[0] & 0xFFFF);
     w.dmin = half_bits_to_float(h0[0] >> 16);
     uint8_t sc[12];
@@ -147,11 +147,11 @@ struct Unit<GGML_Q6_K> {
     ld16_a2(b + 128 + 32 * h, w.qh);
     ld16_a2(b + 128 + 32 * h + 16, w.qh + 4);
     w.d = half_bits_to_float(ld_u16(b + 208));
-    const int8_t* s = (const int8_t*)(b + 192 + 8 * h + 2 * c);
-    w.sc[0] = s[0];
-    w.sc[1] = s[1];
-    w.sc[2] = s[4];
-    w.sc[3] = s[5];
+    const uint8_t* s = b + 192 + 8 * h + 2 * c;
+    w.sc[0] = (int8_t)gload<uint8_t>(s);
+    w.sc[1] = (int8_t)gload<uint8_t>(s + 1);
+    w.sc[2] = (int8_t)gload<uint8_t>(s + 4);
+    w.sc[3] = (int8_t)gload<uint8_t>(s + 5);
     w.c = c;
   }
   __device__ static void qblocks(int u, int& ub0, int& ub1) {
@@ -196,9 +196,9 @@ struct Unit<GGML_IQ3_S> {
     const uint8_t* b = row + (int64_t)(u >> 3) * QBIQ3_S;
     const int ib = u & 7;
     const float d = half_bits_to_float(ld_u16(b));
-    const int nib = (b[106 + ib / 2] >> (4 * (ib & 1))) & 15;
+    const int nib = (gload<uint8_t>(b + 106 + ib / 2) >> (4 * (ib & 1))) & 15;
     w.db = d * (float)(1 + 2 * nib);
-    const int qh = b[66 + ib];
+    const int qh = gload<uint8_t>(b + 66 + ib);
     uint32_t qs[2], sg;
     qs[0] = ld_u32_a2(b + 2 + 8 * ib);
     qs[1] = ld_u32_a2(b + 6 + 8 * ib);

@@ -90,24 +90,30 @@ __device__ __forceinline__ uint32_t f2bf2(float lo, float hi) {
 }
 __device__ __forceinline__ float bf2f(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
 
+// Loads through explicitly global pointers: a weight address read from a slot table is a
+// generic pointer to the compiler, which would otherwise emit flat loads (those also wait
+// on the LDS counter).
+template <typename T>
+__device__ __forceinline__ T gload(const void* p) {
+  return *(const __attribute__((address_space(1))) T*)p;
+}
+
 // little-endian loads from 2-byte aligned addresses (GGUF blocks of 34/110/210 bytes
 // are only 2-byte aligned)
-__device__ __forceinline__ uint16_t ld_u16(const uint8_t* p) { return *(const uint16_t*)p; }
+__device__ __forceinline__ uint16_t ld_u16(const uint8_t* p) { return gload<uint16_t>(p); }
 __device__ __forceinline__ uint32_t ld_u32_a2(const uint8_t* p) {
-  const uint16_t* q = (const uint16_t*)p;
-  return (uint32_t)q[0] | ((uint32_t)q[1] << 16);
+  return (uint32_t)gload<uint16_t>(p) | ((uint32_t)gload<uint16_t>(p + 2) << 16);
 }
 // 16 bytes from a 2-byte aligned address as 4 little-endian dwords
 __device__ __forceinline__ void ld16_a2(const uint8_t* p, uint32_t w[4]) {
-  const uint16_t* q = (const uint16_t*)p;
   uint16_t h[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) h[i] = q[i];
+  for (int i = 0; i < 8; ++i) h[i] = gload<uint16_t>(p + 2 * i);
 #pragma unroll
   for (int i = 0; i < 4; ++i) w[i] = (uint32_t)h[2 * i] | ((uint32_t)h[2 * i + 1] << 16);
 }
 __device__ __forceinline__ void ld16_a16(const uint8_t* p, uint32_t w[4]) {
-  u32x4_t v = *(const u32x4_t*)p;
+  u32x4_t v = gload<u32x4_t>(p);
   w[0] = v[0];
   w[1] = v[1];
   w[2] = v[2];

@@ -18,6 +18,8 @@
 // Reference: the streamer's per-group dequant + cutlass_fused_moe + acc.add_ (P:40789-40819,
 // dequant P:11471-11498), _combine (hot/kt_gguf_hot.py:43-71); the sort-by-expert follows the
 // idea of moe_prepare_ids_kernel (P:31142-31162) with a deterministic stable order.
+#include <type_traits>
+
 #include "bpiece.h"
 #include "kernels.h"
 
@@ -29,25 +31,32 @@ constexpr int CHW = 256;         // routes per wave chunk in the sort
 constexpr int SORT_THREADS = 256;
 constexpr int MAX_SLOTS = 512;
 
-// tile configuration: 8 waves in 2 (M) x 4 (N), each 128 routes x 64 weight rows;
-// tile = 256 routes x 256 weight rows (GATEUP: 128 gate + 128 up rows)
+// tile configuration: 8 waves in 2 (M) x 4 (N), each 128 routes x 64 weight rows (8
+// accumulators of 32 x 32, two waves per SIMD); tile = 256 routes x 256 weight rows
+// (GATEUP: 128 gate + 128 up rows)
 constexpr int BK = 64;
 constexpr int FM = 4, FN = 2, WM = 2, WN = 4;
 constexpr int NTHREADS = WM * WN * 64;
 constexpr int NWAVES = WM * WN;
 constexpr int BM = WM * FM * 32;   // routes per tile
 constexpr int BNW = WN * FN * 32;  // weight rows per tile
-// LDS: A tile double-buffered, 128 B per row (8 swizzled 16-byte slots, no pad), written
-// by direct global->LDS loads; B tile double-buffered, padded rows written by ds_write.
+constexpr int PIECES = 2 * BNW / NTHREADS;  // 32-value B pieces per thread per step
+// LDS: the A tile in ADEPTH buffers (activations prefetched ADEPTH-1 steps ahead by direct
+// global->LDS loads), the B tile (decoded weights) in 2 buffers; rows of 128 B in both,
+// 16-byte slots swizzled (see lds_slot); 3 + 2 buffers fill the 160 KB of LDS, so the
+// IQ3_S kernels (2 KB codebook in LDS) use 2 A buffers.
 constexpr int A_BYTES = BM * BK * 2;
-constexpr int BPITCH = BK + 8;  // bf16 elements per B row
-constexpr int B_BYTES = BNW * BPITCH * 2;
-constexpr int SMEM_AB = 2 * A_BYTES + 2 * B_BYTES;
+constexpr int B_BYTES = BNW * BK * 2;
 constexpr int CPITCH_UP = BNW / 2 + 8;  // epilogue C tile pitches (bf16 elements)
 constexpr int CPITCH_DN = BNW + 8;
 constexpr int SMEM_C = BM * CPITCH_DN * 2;
-constexpr int SMEM = SMEM_AB > SMEM_C ? SMEM_AB : SMEM_C;
-static_assert(SMEM <= 160 * 1024, "LDS");
+template <int TYPE>
+constexpr int adepth() { return TYPE == GGML_IQ3_S ? 2 : 3; }
+template <int TYPE>
+constexpr int smem_bytes() {
+  return adepth<TYPE>() * A_BYTES + 2 * B_BYTES > SMEM_C ? adepth<TYPE>() * A_BYTES + 2 * B_BYTES : SMEM_C;
+}
+static_assert(3 * A_BYTES + 2 * B_BYTES <= 160 * 1024, "LDS");
 
 // ---- route sort by slot. hist is slot-major: hist[e * nch + chunk].
 
@@ -176,13 +185,28 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f +
 // GATEUP = false: A = H rows m0.., Kdim = inter, B rows = down rows c0..c0+BNW,
 //                 out = Y [routes, NI] at row perm[m] (NI = hidden).
 //
-// K loop, one barrier per 64-value step k:
-//   issue A(k+1) global->LDS into Abuf[(k+1)&1], issue the raw B bytes of step k+1;
-//   MFMAs of step k from Abuf[k&1], Bbuf[k&1];
-//   decode B(k+1) (bpiece.h) into Bbuf[(k+1)&1]; wait for the loads; barrier.
-// A rows are 128 B in LDS, 16-byte slot = chunk ^ ((row >> 1) & 7): the 16 lanes of one
-// ds_read_b128 pass (rows r..r+15) then hit 16 different slot/bank groups.
-__device__ __forceinline__ int a_slot(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+// K loop over 64-value steps (bpiece.h maps step positions to row offsets), one barrier
+// per step. Step k: issue A(k+1) global->LDS into Abuf[(k+1)&1] and the raw B bytes of
+// step k+2 into a register ring; MFMAs of step k from Abuf[k&1], Bbuf[k&1] with the decode
+// of B(k+1) (raw bytes loaded a step earlier) into Bbuf[(k+1)&1] in the same basic block,
+// so the scheduler can interleave the decode VALU with the matrix core; wait; barrier.
+// Loads past the last step re-read the last step (clamped, unused), keeping the loop
+// branch-free.
+// Workgroup barrier for the K loop. The caller has already waited for its own LDS writes
+// (s_waitcnt): __syncthreads() would add a workgroup fence that also waits for every
+// outstanding direct global->LDS load, including the ones meant to stay in flight. The
+// wavefront-scope fences only keep the compiler from moving memory operations across.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// A and B rows are 128 B in LDS; the 16-byte slot of chunk c of row r is
+// c ^ (r & 7) ^ ((r >> 3) & 1): any 8 consecutive rows use 8 different slots (no conflict
+// with 32 four-byte banks) and any 16 consecutive rows 16 different (row parity, slot)
+// pairs (no conflict with 64 banks), for the 32-row MFMA operand reads.
+__device__ __forceinline__ int lds_slot(int row, int chunk) { return chunk ^ (row & 7) ^ ((row >> 3) & 1); }
 
 template <int TYPE, bool GATEUP>
 __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restrict__ A_src,
@@ -192,7 +216,7 @@ __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restr
                                                          const uint8_t* __restrict__ W, int w_is_table,
                                                          int64_t w_expert_stride, int64_t rb, int Kdim, int NI,
                                                          int NT, int64_t nblk, uint16_t* __restrict__ out) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[smem_bytes<TYPE>()];
   __shared__ uint32_t grid_lds[TYPE == GGML_IQ3_S ? 512 : 1];
   using BP = BPiece<TYPE>;
 
@@ -222,52 +246,62 @@ __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restr
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const uint8_t* wexp = w_is_table ? (const uint8_t*)((const int64_t*)W)[e] : W + (int64_t)e * w_expert_stride;
+  constexpr int AD = adepth<TYPE>();
   uint8_t* Abuf0 = smem;
-  uint8_t* Bbuf0 = smem + 2 * A_BYTES;
+  uint8_t* Bbuf0 = smem + AD * A_BYTES;
 
   // ---- A sources: direct loads, instruction j of wave w fills rows 8*(NWAVES*j + w) + lane/8
   constexpr int AJ = BM / (8 * NWAVES);
-  int a_off[AJ];  // element offset of this lane's 16-byte chunk (without k0)
+  int a_off[AJ];  // element offset of this lane's 16-byte chunk, without the step base
 #pragma unroll
   for (int j = 0; j < AJ; ++j) {
     const int row = 8 * (NWAVES * j + wave) + (lane >> 3);
-    const int chunk = (lane & 7) ^ ((row >> 1) & 7);
+    const int chunk = lds_slot(row, lane & 7);  // the slot map is an involution per row
     const int r = min(row, valid - 1);
     int src_row;
     if constexpr (GATEUP) src_row = perm[m0 + r] / top_k;
     else src_row = m0 + r;
-    a_off[j] = src_row * Kdim + 8 * chunk;
+    a_off[j] = src_row * Kdim + BP::coff(chunk);
   }
-  auto issue_a = [&](int k0, int buf) {
+  auto issue_a = [&](int sb, auto subc, int buf) {
+    constexpr int SUB = decltype(subc)::value;
+    const int kb = 256 * sb + BP::template ksub<SUB>();
 #pragma unroll
     for (int j = 0; j < AJ; ++j) {
       uint8_t* dst = Abuf0 + buf * A_BYTES + (8 * (NWAVES * j + wave)) * (BK * 2);
-      __builtin_amdgcn_global_load_lds(A_src + a_off[j] + k0, dst, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(A_src + a_off[j] + kb, dst, 16, 0, 0);
     }
   };
 
-  // ---- B source: one 32-value piece per thread (row bj, half bh of the K step)
-  static_assert(BNW * 2 == NTHREADS, "one 32-value B piece per thread");
-  const int bj = tid >> 1, bh = tid & 1;
-  int64_t wr;
-  if constexpr (GATEUP) {
-    const int half = BNW / 2;
-    const int n0 = nt * half;
-    wr = bj < half ? (n0 + bj) : (NI + n0 + (bj - half));
-  } else {
-    wr = (int64_t)nt * BNW + bj;
+  // ---- B source: piece p of thread t is half (q & 1) of weight row q >> 1, q = t * PIECES + p
+  const uint8_t* b_row[PIECES];
+  int b_j[PIECES], b_h[PIECES];
+#pragma unroll
+  for (int p = 0; p < PIECES; ++p) {
+    const int q = tid * PIECES + p;
+    b_j[p] = q >> 1;
+    b_h[p] = q & 1;
+    int64_t wr;
+    if constexpr (GATEUP) {
+      const int half = BNW / 2;
+      const int n0 = nt * half;
+      wr = b_j[p] < half ? (n0 + b_j[p]) : (NI + n0 + (b_j[p] - half));
+    } else {
+      wr = (int64_t)nt * BNW + b_j[p];
+    }
+    b_row[p] = wexp + wr * rb;
   }
-  const uint8_t* b_row = wexp + wr * rb;
-  auto store_b = [&](const uint32_t* breg, int buf) {
-    uint16_t* bd = (uint16_t*)(Bbuf0 + buf * B_BYTES) + bj * BPITCH;
+  auto store_b = [&](const uint32_t* breg, int p, int buf) {
+    uint8_t* bd = Bbuf0 + buf * B_BYTES + b_j[p] * (BK * 2);
+    const int c0 = BP::off0(b_h[p]) / 8, c1 = BP::off1(b_h[p]) / 8;
     u32x4_t v0 = {breg[0], breg[1], breg[2], breg[3]};
     u32x4_t v1 = {breg[4], breg[5], breg[6], breg[7]};
     u32x4_t v2 = {breg[8], breg[9], breg[10], breg[11]};
     u32x4_t v3 = {breg[12], breg[13], breg[14], breg[15]};
-    *(u32x4_t*)(bd + BP::off0(bh)) = v0;
-    *(u32x4_t*)(bd + BP::off0(bh) + 8) = v1;
-    *(u32x4_t*)(bd + BP::off1(bh)) = v2;
-    *(u32x4_t*)(bd + BP::off1(bh) + 8) = v3;
+    *(u32x4_t*)(bd + 16 * lds_slot(b_j[p], c0)) = v0;
+    *(u32x4_t*)(bd + 16 * lds_slot(b_j[p], c0 + 1)) = v1;
+    *(u32x4_t*)(bd + 16 * lds_slot(b_j[p], c1)) = v2;
+    *(u32x4_t*)(bd + 16 * lds_slot(b_j[p], c1 + 1)) = v3;
   };
 
   f32x16_t acc[FM][FN];
@@ -278,27 +312,55 @@ __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restr
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  typename BP::Raw braw;
+  // raw ring: slot (k & 1) holds the bytes of step k (loaded two steps ahead)
+  typename BP::Raw raw[2][PIECES];
   uint32_t breg[16];
-  const int nk = Kdim / BK;
+  const int nsb = Kdim / 256;  // super-block columns, 4 steps each
+  const int lsb = nsb - 1;
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  using S3 = std::integral_constant<int, 3>;
 
   if constexpr (TYPE == GGML_IQ3_S) __syncthreads();
-  issue_a(0, 0);
-  BP::load(b_row, 0, bh, grid_lds, braw);
-  BP::decode(braw, grid_lds, breg);
-  store_b(breg, 0);
+  issue_a(0, S0{}, 0);
+  if constexpr (AD == 3) issue_a(0, S1{}, 1);
+#pragma unroll
+  for (int p = 0; p < PIECES; ++p) {
+    BP::template load<0>(b_row[p], 0, b_h[p], grid_lds, raw[0][p]);
+    BP::template load<1>(b_row[p], 0, b_h[p], grid_lds, raw[1][p]);
+  }
+#pragma unroll
+  for (int p = 0; p < PIECES; ++p) {
+    BP::template decode<0>(raw[0][p], grid_lds, breg);
+    store_b(breg, p, 0);
+  }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  for (int ks = 0; ks < nk; ++ks) {
-    const int buf = ks & 1;
-    const bool more = ks + 1 < nk;
-    if (more) {
-      issue_a((ks + 1) * BK, buf ^ 1);
-      BP::load(b_row, (ks + 1) * BK, bh, grid_lds, braw);
-    }
-    const uint8_t* Ab = Abuf0 + buf * A_BYTES;
-    const uint16_t* Bb = (const uint16_t*)(Bbuf0 + buf * B_BYTES);
+  // step SUB of super-block column sb (step k = 4 sb + SUB); the B buffer parity and the
+  // raw ring slot are SUB & 1, the A buffer is k % AD (abuf). Loads beyond the last step
+  // re-read the last column (in bounds, unused), so the body has no branches.
+  int abuf = 0;
+  auto step = [&](int sb, auto subc) {
+    constexpr int SUB = decltype(subc)::value;
+    constexpr int buf = SUB & 1;
+    constexpr int SUB1 = (SUB + 1) & 3, SUB2 = (SUB + 2) & 3;
+    constexpr int SUBA = (SUB + AD - 1) & 3;  // step k + AD - 1
+    const int sb2 = SUB < 2 ? sb : min(sb + 1, lsb);
+    const int sba = SUB + AD - 1 < 4 ? sb : min(sb + 1, lsb);
+    // raw bytes of step k+2 replace those of step k (decoded one step ago), then the A
+    // tile of step k+AD-1: the A loads are the newest VMEM, so the wait below can leave
+    // just them in flight
+#pragma unroll
+    for (int p = 0; p < PIECES; ++p) BP::template load<SUB2>(b_row[p], sb2, b_h[p], grid_lds, raw[buf][p]);
+    __builtin_amdgcn_sched_barrier(0);
+    int anext = abuf + AD - 1;
+    if (anext >= AD) anext -= AD;
+    issue_a(sba, std::integral_constant<int, SUBA>{}, anext);
+    __builtin_amdgcn_sched_barrier(0);
+    const uint8_t* Ab = Abuf0 + abuf * A_BYTES;
+    const uint8_t* Bb = Bbuf0 + buf * B_BYTES;
 #pragma unroll
     for (int kk = 0; kk < BK; kk += 16) {
       bf16x8_t af[FM], bfr[FN];
@@ -306,9 +368,8 @@ __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restr
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
         const int row = wm * FM * 32 + i * 32 + (lane & 31);
-        af[i] = *(const bf16x8_t*)(Ab + row * (BK * 2) + a_slot(row, chunk) * 16);
+        af[i] = *(const bf16x8_t*)(Ab + row * (BK * 2) + lds_slot(row, chunk) * 16);
       }
-      const int kof = kk + 8 * (lane >> 5);
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         int brow;
@@ -317,21 +378,43 @@ __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restr
         } else {
           brow = wn * FN * 32 + j * 32;
         }
-        bfr[j] = *(const bf16x8_t*)(Bb + (brow + (lane & 31)) * BPITCH + kof);
+        const int row = brow + (lane & 31);
+        bfr[j] = *(const bf16x8_t*)(Bb + row * (BK * 2) + lds_slot(row, chunk) * 16);
       }
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+      // the decode of the next step, spread over the MFMA sub-steps
+      if ((kk / 16) % (4 / PIECES) == 0) {
+        const int p = (kk / 16) / (4 / PIECES);
+        BP::template decode<SUB1>(raw[buf ^ 1][p], grid_lds, breg);
+        store_b(breg, p, buf ^ 1);
+      }
     }
-    if (more) {
-      BP::decode(braw, grid_lds, breg);
-      store_b(breg, buf ^ 1);
+    // A(k+1) has landed once at most the newest AJ VMEM ops (the A loads of step k+2) are
+    // outstanding (vmcnt field in bits 3:0 and 15:14; expcnt 7 and lgkmcnt 15 = no wait);
+    // with AD == 2 everything must land
+    if constexpr (AD == 3) {
+      static_assert(AJ < 16, "vmcnt encoding");
+      __builtin_amdgcn_s_waitcnt(AJ | (7 << 4) | (15 << 8));
+    } else {
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     }
-    __builtin_amdgcn_s_waitcnt(0);  // this thread's A(k+1) direct loads and B stores have landed
-    __syncthreads();
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this thread's B stores
+    lds_barrier();
+    abuf = abuf + 1 == AD ? 0 : abuf + 1;
+  };
+  for (int sb = 0; sb < nsb; ++sb) {
+    step(sb, S0{});
+    step(sb, S1{});
+    step(sb, S2{});
+    step(sb, S3{});
   }
+
+  __builtin_amdgcn_s_waitcnt(0);  // the clamped prefetches of the last steps
+  __syncthreads();
 
   // ---- epilogue through LDS. 32x32 accumulator layout: lane l, element r -> column l%32,
   // row 8*(r/4) + 4*(l/32) + r%4. The C tile is staged as bf16 in LDS, then written out
@@ -457,10 +540,10 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
   const int S = (int)L->n_slots;
   const int64_t K = L->hidden, N = L->inter;
   KTMI_REQUIRE(S >= 1 && S <= MAX_SLOTS, KTMI_EINVAL, "grouped layer: n_slots %d outside [1, %d]", S, MAX_SLOTS);
-  KTMI_REQUIRE(K % BNW == 0 && K % BK == 0, KTMI_EINVAL, "grouped layer: hidden %lld not a multiple of %d",
-               (long long)K, BNW);
-  KTMI_REQUIRE(N % (BNW / 2) == 0 && N % BK == 0, KTMI_EINVAL,
-               "grouped layer: intermediate %lld not a multiple of %d", (long long)N, BNW / 2);
+  KTMI_REQUIRE(K % BNW == 0 && K % 256 == 0, KTMI_EINVAL, "grouped layer: hidden %lld not a multiple of %d",
+               (long long)K, BNW > 256 ? BNW : 256);
+  KTMI_REQUIRE(N % (BNW / 2) == 0 && N % 256 == 0, KTMI_EINVAL,
+               "grouped layer: intermediate %lld not a multiple of 256", (long long)N);
   if (tokens == 0) return KTMI_OK;
   int32_t* hist = (int32_t*)(ws + P.off_counts);
   int32_t* seg = (int32_t*)(ws + P.off_seg);
