@@ -119,7 +119,10 @@ def main():
     ap.add_argument("--tokens", type=int, default=16384)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--cpu-tokens", type=int, default=256, help="tokens of the chunk timed on the CPU")
+    ap.add_argument("--cpu-tokens", type=int, default=1024, help="tokens of the chunk timed on the CPU")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="first run an fp32 negate of MIB MiB (reads and writes exactly MIB MiB), the known-size "
+                         "kernel that scales FETCH_SIZE/WRITE_SIZE counters to bytes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported (this build has no multi-GPU "
@@ -134,6 +137,14 @@ def main():
 
     dev = torch.device("cuda", 0)
     ev = HipEvents()
+    if args.copy_probe:
+        a = torch.ones(args.copy_probe << 18, dtype=torch.float32, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            torch.neg(a, out=b)
+        torch.cuda.synchronize()
+        log(f"copy probe: 3 x neg over {args.copy_probe} MiB")
+        del a, b
     w = S.WORKLOADS[HEADLINE]
     T = args.tokens
     t0 = time.time()
@@ -165,7 +176,8 @@ def main():
     if tfile.exists():
         try:
             tj = json.loads(tfile.read_text())
-            traffic = tj.get(f"{HEADLINE}:T{T}:{dom}")
+            rec = tj.get(f"{HEADLINE}:T{T}:{dom}")
+            traffic = int(rec["bytes"]) if rec else None
         except Exception:  # noqa: BLE001
             traffic = None
 

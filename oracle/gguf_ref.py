@@ -19,7 +19,7 @@ n of trees/flash-next-gguf/sglang-v0.5.19-flash-next-gguf.patch):
   route ................ hot/kt_hot_cache.py:62-75, 121-143
   FFN check ............ P:40821-40853 (_reference_check)
 
-How each part is pinned (tests/test_oracle_*.py):
+How each part is pinned (tests/test_oracle.py, tests/test_host.py):
   * dequant_rows, Q4_K/Q6_K/Q8_0/IQ3_S: (1) the literal restatement of the reference's
     integer vec_dot (`vec_dot_block_literal`, index arithmetic copied in meaning from
     vecdotq.cuh) equals sum(dequant(W) * dequant(q8_1(x))) over random blocks, which

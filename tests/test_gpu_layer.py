@@ -119,3 +119,49 @@ def test_grouped_at_full_shape(dev):
     ref = R.ffn_reference(xb[sample], slot[sample], tw[sample], g, d)
     l2, l1, cos = R.rel_errors(got[sample], ref)
     assert l2 < TOL_REL_L2 and cos > 0.999, (l2, l1, cos)
+
+
+@pytest.mark.parametrize("mode", ["gemv", "grouped"])
+def test_layer_empty_input_and_foreign_ids(dev, mode):
+    """T = 0 is a no-op; slot ids >= S or < -1 (experts owned by no slot here) behave exactly
+    like -1."""
+    import torch
+
+    L, H, _ = _pkg()
+    m = L.MODE_GEMV if mode == "gemv" else L.MODE_GROUPED
+    w, xb, tw, slot, w13, w2 = _case("q4_k+q6_k-h2048-n512-e256-k8-hot40-prefill", 24, 512, 256, 8, 32)
+    W13, W2 = to_dev(w13, dev), to_dev(w2, dev)
+    desc = H.layer_desc(W13, W2, w.hidden, w.inter, w.types[0], w.types[2])
+    y0 = H.moe_layer(desc, bf16_tensor(xb[:0], dev), to_dev(tw[:0], dev), to_dev(slot[:0], dev), m)
+    torch.cuda.synchronize()
+    assert tuple(y0.shape) == (0, w.hidden)
+    rng = np.random.default_rng(11)
+    pick = rng.random(slot.shape) < 0.3
+    foreign = slot.copy()
+    foreign[pick] = np.where(rng.random(int(pick.sum())) < 0.5, w.hot + 5, -7).astype(np.int32)
+    cold = slot.copy()
+    cold[pick] = -1
+    a = _run(dev, w, xb, tw, foreign, w13, w2, m)
+    b = _run(dev, w, xb, tw, cold, w13, w2, m)
+    assert np.array_equal(a, b)
+
+
+def test_grouped_headline_chunk_properties(dev):
+    """The 16384-token prefill chunk at its real shape: a token sample against the fp64 FFN,
+    and two size-independent identities that hold bit-exactly because every route's output
+    depends only on its own row: permuting the tokens permutes the output, and doubling the
+    route weights doubles it."""
+    L, _, _ = _pkg()
+    T = 16384
+    w, xb, tw, slot, w13, w2 = _case("q4_k+q6_k-h2048-n512-e256-k8-hot40-prefill", T)
+    y = _run(dev, w, xb, tw, slot, w13, w2, L.MODE_GROUPED)
+    g, d = dequant_w(w13, w2, w.types, w.hidden, w.inter)
+    sample = np.arange(0, T, 97)
+    ref = R.ffn_reference(xb[sample], slot[sample], tw[sample], g, d)
+    l2, l1, cos = R.rel_errors(R.bf16_to_f32(y[sample]), ref)
+    assert l2 < TOL_REL_L2 and cos > 0.999, (l2, l1, cos)
+    perm = np.random.default_rng(12).permutation(T)
+    yp = _run(dev, w, xb[perm], tw[perm], slot[perm], w13, w2, L.MODE_GROUPED)
+    assert np.array_equal(yp, y[perm])
+    y2 = _run(dev, w, xb, tw * np.float32(2), slot, w13, w2, L.MODE_GROUPED)
+    assert np.array_equal(R.bf16_to_f32(y2), 2 * R.bf16_to_f32(y))

@@ -196,3 +196,34 @@ def test_silu_and_mul_textbook():
 def test_bf16_rounding_ties_to_even():
     x = np.array([1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -(1.0 + 2 ** -8)], np.float32)
     assert np.array_equal(R.bf16_to_f32(R.bf16_bits(x)), np.array([1.0, 1.0 + 2 ** -6, -1.0], np.float32))
+
+
+@pytest.mark.parametrize("types", [(8, 8, 8), (12, 12, 14), (21, 21, 21)])
+def test_cpu_path_agrees_with_ffn_reference(types):
+    """The C restatement of the CPU expert path (Q8_K / Q8_0 int8 dots) against the fp64 FFN
+    over the exactly dequantised weights: quantising activations costs well under 2e-2."""
+    from dataclasses import replace
+
+    import kt_prefill_lend_amd.synth as S
+    from oracle import cpu_moe
+
+    if not cpu_moe.LIB_PATH.exists():
+        pytest.skip("oracle C library not built")
+    base = S.WORKLOADS["q8_0-h2048-n768-e128-k8-hot16"]
+    w = replace(base, hidden=512, inter=256, hot=5, experts=12, types=types)
+    T = 24
+    _, tw, slot, _ = S.routing(w, T)
+    xb = S.activations(w, T)
+    w13, w2 = S.slot_tensors(w)
+    g = R.dequant_rows(w13.reshape(-1, w13.shape[2]), types[0], w.hidden).reshape(w.hot, 2 * w.inter, w.hidden)
+    d = R.dequant_rows(w2.reshape(-1, w2.shape[2]), types[2], w.inter).reshape(w.hot, w.hidden, w.inter)
+    ref = R.ffn_reference(xb, slot, tw, g, d)
+    got = cpu_moe.forward(xb, slot, tw, w13, w2, types[0], types[2], w.inter, threads=2)
+    l2, _, cos = R.rel_errors(got, ref)
+    assert l2 < 2e-2 and cos > 0.999, (l2, cos)
+    # a token with no hot route contributes nothing; the one-thread run is identical
+    slot2 = slot.copy()
+    slot2[0] = -1
+    got2 = cpu_moe.forward(xb, slot2, tw, w13, w2, types[0], types[2], w.inter, threads=1)
+    assert np.all(got2[0] == 0)
+    assert np.array_equal(got2[1:], got[1:])
