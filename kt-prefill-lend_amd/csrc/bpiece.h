@@ -92,8 +92,13 @@ struct BPiece<GGML_Q8_0> {
     const uint8_t* b = row + (8 * sb + 2 * SUB + h) * QB8_0;
     const uint32_t* a = dword_floor(b);
     r.s = byte_shift(b);  // 0 or 2
+    const u32x4_t w0 = gload<u32x4_a4_t>(a), w1 = gload<u32x4_a4_t>(a + 4);
 #pragma unroll
-    for (int i = 0; i < 9; ++i) r.w[i] = gload<uint32_t>(a + i);
+    for (int i = 0; i < 4; ++i) {
+      r.w[i] = w0[i];
+      r.w[4 + i] = w1[i];
+    }
+    r.w[8] = gload<uint32_t>(a + 8);
   }
   template <int SUB>
   __device__ static void decode(const Raw& r, const uint32_t*, uint32_t out[16]) {
@@ -124,15 +129,22 @@ struct BPiece<GGML_Q6_K> {
     r.s = byte_shift(b);
     const uint32_t* ql = dword_floor(b + 64 * hh + 32 * c + 16 * h);
     const uint32_t* qh = dword_floor(b + 128 + 32 * hh + 16 * h);
+    // 16 bytes each from the dword below them: one dwordx4 and the dword after it
+    const u32x4_t l4 = gload<u32x4_a4_t>(ql), h4 = gload<u32x4_a4_t>(qh);
 #pragma unroll
-    for (int i = 0; i < 5; ++i) {
-      r.ql[i] = gload<uint32_t>(ql + i);
-      r.qh[i] = gload<uint32_t>(qh + i);
+    for (int i = 0; i < 4; ++i) {
+      r.ql[i] = l4[i];
+      r.qh[i] = h4[i];
     }
-    const uint8_t* sc = b + 192 + 8 * hh + 2 * c + h;  // scales[8hh + 2c + h], +4 for run c+2
+    r.ql[4] = gload<uint32_t>(ql + 4);
+    r.qh[4] = gload<uint32_t>(qh + 4);
+    // scales[8hh + 2c + h] and scales[8hh + 2c + h + 4] (run c+2) lie in the 8 bytes from
+    // the dword below the first
+    const uint8_t* sc = b + 192 + 8 * hh + 2 * c + h;
     r.sp = 8 * byte_shift(sc);
-    r.sw0 = gload<uint32_t>(dword_floor(sc));
-    r.sw1 = gload<uint32_t>(dword_floor(sc + 4));
+    const u32x2_t s2 = gload<u32x2_a4_t>(dword_floor(sc));
+    r.sw0 = s2[0];
+    r.sw1 = s2[1];
     r.dw = gload<uint32_t>(dword_floor(b + 208));
   }
   template <int SUB>

@@ -186,10 +186,11 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f +
 //                 out = Y [routes, NI] at row perm[m] (NI = hidden).
 //
 // K loop over 64-value steps (bpiece.h maps step positions to row offsets), one barrier
-// per step. Step k: issue A(k+1) global->LDS into Abuf[(k+1)&1] and the raw B bytes of
-// step k+2 into a register ring; MFMAs of step k from Abuf[k&1], Bbuf[k&1] with the decode
-// of B(k+1) (raw bytes loaded a step earlier) into Bbuf[(k+1)&1] in the same basic block,
-// so the scheduler can interleave the decode VALU with the matrix core; wait; barrier.
+// per step. Step k: load the raw B bytes of step k+2 into a register ring; MFMAs of step k
+// from the A buffer k % AD and B buffer k & 1, with the decode of B(k+1) (raw bytes loaded
+// a step earlier) into the other B buffer in the same basic block, so the scheduler can
+// interleave the decode VALU with the matrix core, and the direct global->LDS loads of
+// A(k+AD-1) spread over the sub-steps; wait for A(k+1) and the B stores; barrier.
 // Loads past the last step re-read the last step (clamped, unused), keeping the loop
 // branch-free.
 // Workgroup barrier for the K loop. The caller has already waited for its own LDS writes
@@ -263,11 +264,11 @@ __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restr
     else src_row = m0 + r;
     a_off[j] = src_row * Kdim + BP::coff(chunk);
   }
-  auto issue_a = [&](int sb, auto subc, int buf) {
+  auto issue_a = [&](int sb, auto subc, int buf, int j0 = 0, int j1 = AJ) {
     constexpr int SUB = decltype(subc)::value;
     const int kb = 256 * sb + BP::template ksub<SUB>();
 #pragma unroll
-    for (int j = 0; j < AJ; ++j) {
+    for (int j = j0; j < j1; ++j) {
       uint8_t* dst = Abuf0 + buf * A_BYTES + (8 * (NWAVES * j + wave)) * (BK * 2);
       __builtin_amdgcn_global_load_lds(A_src + a_off[j] + kb, dst, 16, 0, 0);
     }
@@ -354,15 +355,22 @@ __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restr
     // just them in flight
 #pragma unroll
     for (int p = 0; p < PIECES; ++p) BP::template load<SUB2>(b_row[p], sb2, b_h[p], grid_lds, raw[buf][p]);
-    __builtin_amdgcn_sched_barrier(0);
     int anext = abuf + AD - 1;
     if (anext >= AD) anext -= AD;
-    issue_a(sba, std::integral_constant<int, SUBA>{}, anext);
-    __builtin_amdgcn_sched_barrier(0);
     const uint8_t* Ab = Abuf0 + abuf * A_BYTES;
     const uint8_t* Bb = Bbuf0 + buf * B_BYTES;
 #pragma unroll
     for (int kk = 0; kk < BK; kk += 16) {
+      // the A loads of step k+AD-1 go out over the last three MFMA sub-steps: the waves
+      // leave the barrier together, and one burst of every wave's loads would queue them
+      // behind each other at the address unit
+      if (kk >= 16) {
+        constexpr int NPART = 3;
+        const int part = kk / 16 - 1;
+        __builtin_amdgcn_sched_barrier(0);
+        issue_a(sba, std::integral_constant<int, SUBA>{}, anext, part * AJ / NPART, (part + 1) * AJ / NPART);
+        __builtin_amdgcn_sched_barrier(0);
+      }
       bf16x8_t af[FM], bfr[FN];
       const int chunk = (kk >> 3) + (lane >> 5);
 #pragma unroll
