@@ -180,7 +180,9 @@ static int check_layer(const ktmi_layer* L) {
 int64_t ktmi_moe_layer_workspace(const ktmi_layer* L, int64_t tokens, int64_t top_k, int mode) {
   if (!L || tokens < 0 || top_k <= 0) return 0;
   if (mode == KTMI_MODE_AUTO) mode = ktmi_moe_layer_mode(L, tokens, top_k);
-  if (mode == KTMI_MODE_GEMV) return gemv_layer_workspace(L, tokens, top_k);
+  if (mode == KTMI_MODE_GEMV)
+    return decode_layer_fits(L, tokens, top_k) ? decode_layer_workspace(L, tokens, top_k)
+                                               : gemv_layer_workspace(L, tokens, top_k);
   return grouped_plan(tokens, top_k, L->n_slots, L->hidden, L->inter).total;
 }
 
@@ -202,6 +204,9 @@ int ktmi_moe_layer(const ktmi_layer* L, const void* x, const float* topk_w, cons
   hipStream_t s = (hipStream_t)stream;
   const int64_t R = tokens * top_k;
   const int64_t K = L->hidden, N = L->inter;
+  if (mode == KTMI_MODE_GEMV && decode_layer_fits(L, tokens, top_k))
+    return launch_decode_layer(L, (const uint16_t*)x, topk_w, slot_ids, tokens, top_k, (uint16_t*)y,
+                               (uint8_t*)workspace, s);
   if (mode == KTMI_MODE_GEMV) {
     KTMI_REQUIRE(R <= 65535, KTMI_EINVAL, "moe_layer: GEMV mode takes at most 65535 routes");
     auto al = [](int64_t v) { return (v + 255) & ~(int64_t)255; };
