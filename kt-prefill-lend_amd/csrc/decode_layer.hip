@@ -34,7 +34,8 @@ constexpr int DEC_RG = 32;     // intermediate rows per gate/up block (one q8_1 
 constexpr int DEC_DR = 8;      // hidden rows per down block
 constexpr int DEC_SPW = 4;     // slots per wave and round in the down block (8 lanes per row)
 constexpr int DEC_MAX_UNITS = 64;    // gate/up: weight units per row
-constexpr int DEC_MCH_MAX = 16;      // member routes per pass of the gate/up block
+constexpr int DEC_MCH_MAX = 16;      // member routes per pass of the gate/up block, at most
+constexpr int DEC_MCH_CHUNK = 8;     // member routes per gate/up block and pass
 constexpr int DEC_MAX_UNITS2 = 16;   // down: weight units per row
 
 __device__ __forceinline__ float bf16_round(float v) { return (float)(__bf16)v; }
@@ -60,10 +61,12 @@ __device__ __forceinline__ float group_sum(float v) {
 // lanes per row of the down block: 8, or 16 for rows of 16 units (each lane one unit)
 __host__ __device__ constexpr int dec_lpr(int units) { return units >= 16 ? 16 : 8; }
 
-// One block per (slot e, group g of 32 intermediate rows): 512 threads = 64 rows (32 gate
-// rows 32g.., 32 up rows N+32g..) x 8 lanes; lane j of a row holds units j, j+8, ... of it
-// (UPL of them). Every weight unit is loaded into registers before any
-// activation is touched, then each member route (a route of slot e) streams past them.
+// One block per (slot e, group g of 32 intermediate rows, member chunk z): 512 threads = 64
+// rows (32 gate rows 32g.., 32 up rows N+32g..) x 8 lanes; lane j of a row holds units j,
+// j+8, ... of it (UPL of them). Every weight unit is loaded into registers before any
+// activation is touched, then the block's member routes (routes of slot e; chunks z,
+// z + gridDim.z, ... of mch routes) stream past them. Splitting a popular slot's routes
+// over gridDim.z blocks keeps its rows from serialising the kernel.
 template <int TYPE, int UPL>
 __global__ __launch_bounds__(DEC_THREADS) void decode_gate_up(const __bf16* __restrict__ x, int K, int N,
                                                               const int32_t* __restrict__ slot_ids, int top_k, int R,
@@ -75,84 +78,107 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_gate_up(const __bf16* __re
   static_assert(DEC_THREADS / LPR == 2 * DEC_RG, "one row per thread group");
   extern __shared__ __attribute__((aligned(16))) uint8_t xq_lds[];  // mch q8_1 rows of K
   __shared__ int mem[DEC_MAX_ROUTES];
-  __shared__ int nm_s;
+  __shared__ int wcnt[DEC_WAVES];
   __shared__ float gu[DEC_MCH_MAX][2 * DEC_RG];
+  __shared__ int2 xs_lds[DEC_MCH_MAX * DEC_MAX_UNITS * 2];  // int8 sums of q8_1 half-blocks
   __shared__ uint32_t grid[TYPE == GGML_IQ3_S ? 512 : 1];
   const int e = blockIdx.x, g = blockIdx.y;
   const int tid = threadIdx.x;
-  if (tid == 0) nm_s = 0;
-  __syncthreads();
-  for (int p = tid; p < R; p += DEC_THREADS)
-    if (slot_ids[p] == e) mem[atomicAdd(&nm_s, 1)] = p;
+  // the routes of slot e in ascending order (every block of the slot sees the same list,
+  // so the member chunks split over gridDim.z are disjoint): thread p tests route p
+  static_assert(DEC_MAX_ROUTES <= DEC_THREADS, "one route per thread");
+  const int lane = tid & 63, wv = tid >> 6;
+  const bool hit = tid < R && slot_ids[tid] == e;
+  const uint64_t bal = __ballot(hit);
+  if (lane == 0) wcnt[wv] = __popcll(bal);
   if constexpr (TYPE == GGML_IQ3_S) stage_iq3s_grid(grid);
   __syncthreads();
-  const int nm = nm_s;
-  if (nm == 0) return;  // uniform: no route of this slot
+  int base = 0, nm = 0;
+#pragma unroll
+  for (int k = 0; k < DEC_WAVES; ++k) {
+    base += k < wv ? wcnt[k] : 0;
+    nm += wcnt[k];
+  }
+  if (hit) mem[base + __popcll(bal & ((1ull << lane) - 1))] = tid;
+  __syncthreads();
+  const int cz = blockIdx.z, nz = gridDim.z;
+  if (cz * mch >= nm) return;  // uniform: no route of this slot (or of this chunk)
   const int64_t rb = row_bytes(K, TYPE);
   const uint8_t* wexp = w_is_table ? (const uint8_t*)((const int64_t*)W13)[e] : W13 + (int64_t)e * w_stride;
   const int i = tid / LPR, j0 = tid % LPR;
   const int row = i < DEC_RG ? g * DEC_RG + i : N + g * DEC_RG + (i - DEC_RG);
   const uint8_t* wrow = wexp + (int64_t)row * rb;
   const int units = K / U::VALS;
+  const int Kp = (int)q8_1_cols_padded(K);
+  const int xq_row = Kp / 32 * QB8_1;
+  const int KB = Kp / 32;  // q8_1 blocks per row; mch * KB <= DEC_THREADS: one block per thread
+  // q8_1 of the members' x rows, one thread per 32-value block (d and q as the quantize_q8_1
+  // kernel; the header's fp16 sum field, which no unit reads, is summed in index order here).
+  // Split in two so the first chunk's x loads go out before the weight loads, and the
+  // weights are unpacked only after the quantisation.
+  u32x4_t xr[4];
+  auto load_x = [&](int c0, int nc) {
+    const int m = tid / KB, kb = tid % KB;
+    if (m < nc && kb * 32 < K) {
+      const __bf16* src = x + (int64_t)(mem[c0 + m] / top_k) * K + kb * 32;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) xr[c] = gload<u32x4_t>(src + 8 * c);
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) xr[c] = u32x4_t{0u, 0u, 0u, 0u};
+    }
+  };
+  auto quantize_x = [&](int nc) {
+    const int m = tid / KB, kb = tid % KB;
+    if (m >= nc) return;
+    int2 hs = {0, 0};
+    float v[32];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        v[8 * c + 2 * t] = __uint_as_float(xr[c][t] << 16);
+        v[8 * c + 2 * t + 1] = __uint_as_float(xr[c][t] & 0xFFFF0000u);
+      }
+    float amax = 0.0f, sum = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 32; ++t) {
+      amax = fmaxf(amax, fabsf(v[t]));
+      sum += v[t];
+    }
+    const float d = amax / 127.0f;
+    uint8_t* blk = xq_lds + m * xq_row + kb * QB8_1;
+    *(uint32_t*)blk = (uint32_t)float_to_half_bits(d) | ((uint32_t)float_to_half_bits(sum) << 16);
+#pragma unroll
+    for (int q8 = 0; q8 < 8; ++q8) {
+      uint32_t wd = 0;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int8_t q = amax == 0.0f ? 0 : (int8_t)roundf(v[4 * q8 + t] / d);
+        wd |= (uint32_t)(uint8_t)q << (8 * t);
+        if (q8 < 4) hs.x += q; else hs.y += q;
+      }
+      *(uint32_t*)(blk + 4 + 4 * q8) = wd;
+    }
+    xs_lds[m * KB + kb] = hs;
+  };
+  load_x(cz * mch, min(mch, nm - cz * mch));
+  __builtin_amdgcn_sched_barrier(0);
   typename U::W w[UPL];
 #pragma unroll
   for (int j = 0; j < UPL; ++j)
     if (j0 + LPR * j < units) U::load(wrow, j0 + LPR * j, grid, w[j]);
-  const int Kp = (int)q8_1_cols_padded(K);
-  const int xq_row = Kp / 32 * QB8_1;
-  const int KB = Kp / 32;  // q8_1 blocks per row
-  bool finished = false;
-  for (int c0 = 0; c0 < nm; c0 += mch) {
+  __builtin_amdgcn_sched_barrier(0);
+  quantize_x(min(mch, nm - cz * mch));
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < UPL; ++j)
+    if (j0 + LPR * j < units) U::finish(w[j], grid);
+  for (int c0 = cz * mch; c0 < nm; c0 += nz * mch) {
     const int nc = min(mch, nm - c0);
-    // q8_1 of the members' x rows, one thread per 32-value block (d and q as the
-    // quantize_q8_1 kernel; the header's fp16 sum field, which no unit reads, is summed in
-    // index order here)
-    for (int b = tid; b < nc * KB; b += DEC_THREADS) {
-      const int m = b / KB, kb = b % KB;
-      uint8_t* blk = xq_lds + m * xq_row + kb * QB8_1;
-      float v[32];
-      if (kb * 32 < K) {
-        const __bf16* src = x + (int64_t)(mem[c0 + m] / top_k) * K + kb * 32;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const u32x4_t q4 = gload<u32x4_t>(src + 8 * c);
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            v[8 * c + 2 * t] = __uint_as_float(q4[t] << 16);
-            v[8 * c + 2 * t + 1] = __uint_as_float(q4[t] & 0xFFFF0000u);
-          }
-        }
-      } else {
-#pragma unroll
-        for (int t = 0; t < 32; ++t) v[t] = 0.0f;
-      }
-      float amax = 0.0f, sum = 0.0f;
-#pragma unroll
-      for (int t = 0; t < 32; ++t) {
-        amax = fmaxf(amax, fabsf(v[t]));
-        sum += v[t];
-      }
-      const float d = amax / 127.0f;
-      uint32_t packed[8];
-#pragma unroll
-      for (int q8 = 0; q8 < 8; ++q8) {
-        uint32_t wd = 0;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const int8_t q = amax == 0.0f ? 0 : (int8_t)roundf(v[4 * q8 + t] / d);
-          wd |= (uint32_t)(uint8_t)q << (8 * t);
-        }
-        packed[q8] = wd;
-      }
-      *(uint32_t*)blk = (uint32_t)float_to_half_bits(d) | ((uint32_t)float_to_half_bits(sum) << 16);
-#pragma unroll
-      for (int q8 = 0; q8 < 8; ++q8) *(uint32_t*)(blk + 4 + 4 * q8) = packed[q8];
-    }
-    if (!finished) {
-#pragma unroll
-      for (int j = 0; j < UPL; ++j)
-        if (j0 + LPR * j < units) U::finish(w[j], grid);
-      finished = true;
+    if (c0 > cz * mch) {
+      load_x(c0, nc);
+      quantize_x(nc);
     }
     __syncthreads();
     for (int m = 0; m < nc; ++m) {
@@ -165,7 +191,17 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_gate_up(const __bf16* __re
           U::qblocks(u, ub0, ub1);
           Act<U::NQ> a;
           load_act<U::NQ>(xq_lds + m * xq_row, ub0, ub1, a);
-          U::prep(a);
+          // the int8 sums the units need (Unit::prep), computed once per block in quantize_x
+          const int2 s0 = xs_lds[m * KB + ub0], s1 = xs_lds[m * KB + ub1];
+          if constexpr (TYPE == GGML_Q4_K) {
+            a.s[0] = s0.x + s0.y;
+            a.s[1] = s1.x + s1.y;
+          } else if constexpr (TYPE == GGML_Q6_K) {
+            a.s[0] = s0.x;
+            a.s[1] = s0.y;
+            a.s[2] = s1.x;
+            a.s[3] = s1.y;
+          }
           v += U::dot(w[j], a);
         }
       }
@@ -324,9 +360,14 @@ int launch_gate_up(const __bf16* x, int64_t K, int64_t N, const int32_t* slot_id
                    int64_t S, const uint8_t* W13, int w_is_table, int64_t w_stride, uint8_t* hq, int64_t hq_stride,
                    hipStream_t stream) {
   const int64_t xq_row = q8_1_row_bytes(K);
-  const int mch = (int)(DEC_MAX_XQ_LDS / xq_row < DEC_MCH_MAX ? DEC_MAX_XQ_LDS / xq_row : DEC_MCH_MAX);
+  int mch = (int)(DEC_MAX_XQ_LDS / xq_row < DEC_MCH_CHUNK ? DEC_MAX_XQ_LDS / xq_row : DEC_MCH_CHUNK);
+  const int kb = (int)(q8_1_cols_padded(K) / 32);
+  if (mch * kb > DEC_THREADS) mch = DEC_THREADS / kb;  // one q8_1 block per thread and chunk
   const size_t lds = (size_t)mch * (size_t)xq_row;
-  dim3 grid((unsigned)S, (unsigned)(N / DEC_RG));
+  // one block per row group walks all of a slot's routes: splitting them over more blocks
+  // (gridDim.z) re-reads the weights once per extra block, which costs more than it saves
+  // at decode sizes
+  dim3 grid((unsigned)S, (unsigned)(N / DEC_RG), 1);
 #define KTMI_GU(P)                                                                                          \
   decode_gate_up<TYPE, P><<<grid, DEC_THREADS, lds, stream>>>(x, (int)K, (int)N, slot_ids, (int)top_k, (int)R, \
                                                                (int)S, W13, w_is_table, w_stride, hq, hq_stride, mch)

@@ -113,14 +113,24 @@ struct Unit<GGML_Q4_K> {
       w.q[4 + i] = v1[i];
     }
   }
+  // 6-bit scale and min of sub-block j = 2g + k (k = 0, 1) from the 12 scale bytes in words
+  // w1 (bytes 0-3), w2 (4-7), w3 (8-11): j < 4: scales[j] & 63 and scales[j+4] & 63;
+  // j >= 4: low 4 bits from scales[j+4], high 2 bits from bits 6-7 of scales[j-4] (scale)
+  // and scales[j] (min). Shifts and selects only, for a runtime g.
+  __device__ static void scale_min(uint32_t w1, uint32_t w2, uint32_t w3, int j, int& sc, int& m) {
+    const uint32_t sh = 8 * (j & 3);
+    const uint32_t b1 = (w1 >> sh) & 0xFF, b2 = (w2 >> sh) & 0xFF, b3 = (w3 >> sh) & 0xFF;
+    const int lo_sc = (int)(b1 & 63), lo_m = (int)(b2 & 63);
+    const int hi_sc = (int)((b3 & 15) | ((b1 >> 6) << 4));
+    const int hi_m = (int)((b3 >> 4) | ((b2 >> 6) << 4));
+    sc = j < 4 ? lo_sc : hi_sc;
+    m = j < 4 ? lo_m : hi_m;
+  }
   __device__ static void finish(W& w, const uint32_t*) {
     w.d = half_bits_to_float(w.h0[0] & 0xFFFF);
     w.dmin = half_bits_to_float(w.h0[0] >> 16);
-    uint8_t sc[12];
-#pragma unroll
-    for (int i = 0; i < 12; ++i) sc[i] = (w.h0[1 + i / 4] >> (8 * (i % 4))) & 0xFF;
-    q4k_scale_min(sc, 2 * w.g, w.sc0, w.m0);
-    q4k_scale_min(sc, 2 * w.g + 1, w.sc1, w.m1);
+    scale_min(w.h0[1], w.h0[2], w.h0[3], 2 * w.g, w.sc0, w.m0);
+    scale_min(w.h0[1], w.h0[2], w.h0[3], 2 * w.g + 1, w.sc1, w.m1);
   }
   __device__ static void qblocks(int u, int& ub0, int& ub1) {
     ub0 = 8 * (u >> 2) + 2 * (u & 3);
