@@ -26,6 +26,7 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 HEADLINE = "q4_k+q6_k-h2048-n512-e256-k8-hot40-prefill"
 DECODE = "q4_k-h2048-n512-e256-k8-hot32-decode"
+STREAM = "q4_k+q6_k-h7168-n2048-e256-k8-hot24-stream4"
 STAGES = ["prep", "gate_up", "mid", "down", "combine"]
 
 
@@ -126,6 +127,7 @@ def main():
     ap.add_argument("--tokens", type=int, default=16384)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-stream", action="store_true", help="skip the streamed-layers leg")
     ap.add_argument("--cpu-tokens", type=int, default=1024, help="tokens of the chunk timed on the CPU")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run an fp32 negate of MIB MiB (reads and writes exactly MIB MiB), the known-size "
@@ -214,6 +216,9 @@ def main():
     if not args.no_decode:
         result["decode"] = bench_decode(P, torch, S, ev, dev)
 
+    if not args.no_stream:
+        result["stream"] = bench_stream(P, torch, S, ev, dev)
+
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(S, w, args.cpu_tokens, T)
 
@@ -253,6 +258,76 @@ def bench_decode(P, torch, S, ev, dev, steps=50, warmup=5):
         res[f"T{T}"] = {"hot_routes": int((slot >= 0).sum()), "unique_experts": uniq, "bytes": nbytes, **out}
         log(f"decode T={T}: {res[f'T{T}']}")
     del copies
+    return res
+
+
+def bench_stream(P, torch, S, ev, dev, distinct=2, reps=3):
+    """Large-expert layers streamed from pinned host memory (hidden 7168, intermediate 2048,
+    24 hot Q4_K/Q6_K experts per layer, 6144-token chunk, 4 layers): each layer's experts
+    are one group; layer l+1's copy overlaps layer l's grouped layer. Weights: `distinct`
+    quantised experts repeated over the 24 slots (the bytes moved and the work are those of
+    24 experts). Reports the H2D copy time per layer, the compute time per layer on resident
+    weights, the pipelined time of the 4 layers, and the overlap efficiency
+    (serial - pipelined) / (serial - ideal), ideal = max(copies, computes) + min(copy, compute)."""
+    import kt_prefill_lend_amd.kt_stream_prefill as SP
+
+    H, L = P.kt_gguf_hot, P._lib
+    w = S.WORKLOADS[STREAM]
+    T = w.tokens[0]
+    nl = w.layers
+    t0 = time.time()
+    parts = [S.expert_weights(w, e, 0, 16) for e in range(distinct)]
+    w13 = np.stack([parts[e % distinct][0] for e in range(w.hot)])
+    w2 = np.stack([parts[e % distinct][1] for e in range(w.hot)])
+    banks = [SP.Bank.from_slot_rows(torch.from_numpy(w13), torch.from_numpy(w2), w.inter, w.types) for _ in range(nl)]
+    ids, tw, slot, _ = S.routing(w, T)
+    x = torch.from_numpy(S.activations(w, T).view(np.int16)).to(dev).view(torch.bfloat16)
+    tw_d, slot_d = torch.from_numpy(tw).to(dev), torch.from_numpy(slot).to(dev)
+    log(f"stream: {nl} layers x {w.hot} experts, {banks[0].gate.nbytes * 2 + banks[0].down.nbytes:,} B per layer pinned,"
+        f" prepared in {time.time() - t0:.1f}s")
+    st = SP.KTStreamPrefillGGUF(w.inter, w.hidden, w.top_k, w.types, group_size=w.hot, device=dev)
+    for i, b in enumerate(banks):
+        st.set_bank(i, b)
+    stream = L.stream_ptr(dev)
+    # copies alone (copy stream, host wall clock around a synchronised batch)
+    st.sync_copies()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for r in range(reps):
+        for i in range(nl):
+            st._stage((r * nl + i) % 2, i, 0, w.hot)
+    st.sync_copies()
+    copy_ms = (time.perf_counter() - t1) * 1e3 / (reps * nl)
+    layer_bytes = banks[0].gate.nbytes * 2 + banks[0].down.nbytes
+    # compute alone, on resident weights
+    W13, W2 = torch.from_numpy(w13).to(dev), torch.from_numpy(w2).to(dev)
+    desc = H.layer_desc(W13, W2, w.hidden, w.inter, w.types[0], w.types[2])
+    ms_c, _, _ = time_layer(P, torch, [desc], x, tw_d, slot_d, L.MODE_GROUPED, reps * nl, 2, ev, breakdown_steps=1)
+    del W13, W2
+    # the pipeline: nl layers, one group each
+    items = [(i, x, tw_d, slot_d) for i in range(nl)]
+    st.run_layers(items)  # warm
+    torch.cuda.synchronize()
+    se = ev.create(2)
+    ev.record(se[0], stream)
+    for _ in range(reps):
+        st.run_layers(items)
+    ev.record(se[1], stream)
+    torch.cuda.synchronize()
+    total = ev.ms(se[0], se[1]) / reps
+    ev.destroy(se)
+    st.close()
+    serial = nl * (copy_ms + ms_c)
+    ideal = max(nl * copy_ms, nl * ms_c) + min(copy_ms, ms_c)
+    eff = (serial - total) / (serial - ideal) if serial > ideal else 1.0
+    r_hot = int((slot >= 0).sum())
+    res = {"workload": w.name, "tokens": T, "layers": nl, "hot_routes": r_hot, "layer_bytes": layer_bytes,
+           "copy_ms_per_layer": round(copy_ms, 3), "h2d_GBps": round(layer_bytes / (copy_ms * 1e-3) / 1e9, 1),
+           "compute_ms_per_layer": round(ms_c, 3),
+           "compute_TFLOPs": round(6.0 * w.hidden * w.inter * r_hot / (ms_c * 1e-3) / 1e12, 1),
+           "pipelined_ms": round(total, 3), "serial_ms": round(serial, 3), "ideal_ms": round(ideal, 3),
+           "overlap_efficiency": round(eff, 3)}
+    log(f"stream: {res}")
     return res
 
 

@@ -148,6 +148,52 @@ int ktmi_set_stage_events(void* const* events, int n);
  * the GGUF files the reference loads are produced by llama.cpp's quantisers. */
 int ktmi_quantize_rows_host(const float* x, int64_t rows, int64_t cols, int ggml_type, void* out, int threads);
 
+/* ---- layer-weight streamer (P:40543-40550 _Slot, P:40773-40787 _stage, P:40928-40992 run).
+ * Experts' raw GGUF bytes move from pinned host banks into double-buffered device slots on
+ * a copy stream of its own while the compute stream runs the grouped layer on the other
+ * slot. A slot holds up to max_group experts as w13 [n, 2N, row bytes] (gate rows, then up
+ * rows) and w2 [n, K, row bytes]: the layout ktmi_layer reads (hot/kt_gguf_hot.py:17-21). */
+#define KTMI_STREAM_MAX_SLOTS 4
+typedef struct ktmi_streamer ktmi_streamer;
+
+/* One layer's pinned host copy of n_experts experts, one array per projection with each
+ * expert's bytes contiguous: the reference's _bank (P:40700-40752, [E, part bytes]). */
+typedef struct ktmi_bank {
+  const void* gate; /* host [n_experts, part_gate] */
+  const void* up;   /* host [n_experts, part_up]; part_up == part_gate */
+  const void* down; /* host [n_experts, part_down] */
+  int64_t part_gate, part_up, part_down;
+  int64_t n_experts;
+} ktmi_bank;
+
+/* Allocates n_slots (2..KTMI_STREAM_MAX_SLOTS) device slots of max_group experts
+ * (part13 = gate + up bytes and part2 = down bytes per expert) and the copy stream, on the
+ * current device. Replaces preallocate() / _Slot (P:40607-40636, 40543-40550). NULL on
+ * failure (ktmi_last_error). */
+ktmi_streamer* ktmi_streamer_create(int64_t max_group, int64_t part13, int64_t part2, int n_slots);
+int ktmi_streamer_destroy(ktmi_streamer* s);
+/* device pointers of slot `slot`'s w13 and w2 */
+int ktmi_streamer_slot(ktmi_streamer* s, int slot, void** w13, void** w2);
+/* Copies experts [first, first+n) of `bank` into `slot` on the copy stream, after the
+ * compute stream's last release of the slot; the slot's loaded event follows the copies.
+ * Replaces _stage (P:40773-40787). */
+int ktmi_streamer_stage(ktmi_streamer* s, int slot, const ktmi_bank* bank, int64_t first, int64_t n);
+/* `stream` waits until the slot's last staging has landed (cur.wait_event(dma_done), P:40976). */
+int ktmi_streamer_acquire(ktmi_streamer* s, int slot, void* stream);
+/* marks the slot free once `stream` reaches this point (compute_done.record, P:40978) */
+int ktmi_streamer_release(ktmi_streamer* s, int slot, void* stream);
+/* host wait for every copy staged so far */
+int ktmi_streamer_sync(ktmi_streamer* s);
+/* out[i] = ids[i] - base if base <= ids[i] < base + count, else -1: a group's local slot
+ * ids (the reference's `local`, P:40798). */
+int ktmi_remap_ids(const int32_t* ids, int64_t n, int32_t base, int32_t count, int32_t* out, void* stream);
+/* acc[i] = bf16(acc[i] + x[i]) for bf16 arrays (acc.add_(out), P:40819); 16-byte aligned */
+int ktmi_add_bf16(void* acc, const void* x, int64_t n, void* stream);
+/* pinned host memory for banks (hipHostMalloc; the reference pins through kt_pinned,
+ * P:39462-39586). NULL on failure. */
+void* ktmi_host_alloc(int64_t bytes);
+int ktmi_host_free(void* p);
+
 #ifdef __cplusplus
 }
 #endif

@@ -34,6 +34,18 @@ class ktmi_layer(C.Structure):
     ]
 
 
+class ktmi_bank(C.Structure):
+    _fields_ = [
+        ("gate", C.c_void_p),
+        ("up", C.c_void_p),
+        ("down", C.c_void_p),
+        ("part_gate", C.c_int64),
+        ("part_up", C.c_int64),
+        ("part_down", C.c_int64),
+        ("n_experts", C.c_int64),
+    ]
+
+
 # name -> (restype, argtypes); every symbol declared in include/ktmi.h
 SIGNATURES = {
     "ktmi_last_error": (C.c_char_p, []),
@@ -53,6 +65,17 @@ SIGNATURES = {
     "ktmi_moe_layer_mode": (_i32, [C.POINTER(ktmi_layer), _i64, _i64]),
     "ktmi_set_stage_events": (_i32, [C.POINTER(C.c_void_p), _i32]),
     "ktmi_quantize_rows_host": (_i32, [_vp, _i64, _i64, _i32, _vp, _i32]),
+    "ktmi_streamer_create": (_vp, [_i64, _i64, _i64, _i32]),
+    "ktmi_streamer_destroy": (_i32, [_vp]),
+    "ktmi_streamer_slot": (_i32, [_vp, _i32, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p)]),
+    "ktmi_streamer_stage": (_i32, [_vp, _i32, C.POINTER(ktmi_bank), _i64, _i64]),
+    "ktmi_streamer_acquire": (_i32, [_vp, _i32, _vp]),
+    "ktmi_streamer_release": (_i32, [_vp, _i32, _vp]),
+    "ktmi_streamer_sync": (_i32, [_vp]),
+    "ktmi_remap_ids": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp]),
+    "ktmi_add_bf16": (_i32, [_vp, _vp, _i64, _vp]),
+    "ktmi_host_alloc": (_vp, [_i64]),
+    "ktmi_host_free": (_i32, [_vp]),
 }
 
 _lib = None

@@ -36,6 +36,7 @@ namespace ktmi {
 
 // set by host entry points; returned by ktmi_last_error()
 void set_error(const char* fmt, ...);
+void clear_error();
 
 #define KTMI_HIP_TRY(expr)                                                               \
   do {                                                                                   \

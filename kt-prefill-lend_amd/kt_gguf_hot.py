@@ -63,6 +63,8 @@ def _reader(path: str):
 
 def layer_desc(w13: torch.Tensor, w2: torch.Tensor, hidden: int, inter: int, type13: int, type2: int,
                table: bool = False) -> _lib.ktmi_layer:
+    """The C descriptor of a layer's slot tensors. It holds raw device pointers: the caller
+    keeps w13 and w2 alive for as long as the descriptor is used."""
     L = _lib.ktmi_layer()
     L.hidden, L.inter = hidden, inter
     L.n_slots = w13.shape[0]

@@ -159,3 +159,32 @@ def test_cpu_mask_hook(monkeypatch):
 
     ids = torch.tensor([[0, 5], [2, 3]])
     assert W.mask_cpu_expert_ids(ids, 3).tolist() == [[0, -1], [2, -1]]
+
+
+def test_stream_bank_validation_and_threshold(monkeypatch):
+    import torch
+
+    import kt_prefill_lend_amd.kt_stream_prefill as SP
+
+    N, K = 256, 512
+    types = (12, 12, 14)
+    pg, pu, pd = SP.part_bytes(types, N, K)
+    assert (pg, pu, pd) == (N * (K // 256) * 144, N * (K // 256) * 144, K * (N // 256) * 210)
+    ok = SP.Bank(torch.zeros((3, pg), dtype=torch.uint8), torch.zeros((3, pu), dtype=torch.uint8),
+                 torch.zeros((3, pd), dtype=torch.uint8), types)
+    assert ok.n_experts == 3
+    with pytest.raises(RuntimeError):
+        SP.Bank(torch.zeros((3, pg), dtype=torch.int16), torch.zeros((3, pu), dtype=torch.uint8),
+                torch.zeros((3, pd), dtype=torch.uint8), types)
+    with pytest.raises(RuntimeError):
+        SP.Bank(torch.zeros((3, pg), dtype=torch.uint8), torch.zeros((2, pu), dtype=torch.uint8),
+                torch.zeros((3, pd), dtype=torch.uint8), types)
+    with pytest.raises(RuntimeError, match="gate/up types"):
+        SP.Bank(torch.zeros((3, pg), dtype=torch.uint8), torch.zeros((3, pu), dtype=torch.uint8),
+                torch.zeros((3, pd), dtype=torch.uint8), (12, 14, 14))
+    monkeypatch.setattr(SP, "STREAM_THRESHOLD", 0)
+    assert SP.stream_prefill_for(N, K, 8, types, 100000) is None
+    monkeypatch.setattr(SP, "STREAM_THRESHOLD", 4096)
+    monkeypatch.setattr(SP, "preallocate", lambda *a, **k: "streamer")
+    assert SP.stream_prefill_for(N, K, 8, types, 1024) is None
+    assert SP.stream_prefill_for(N, K, 8, types, 8192) == "streamer"
