@@ -289,15 +289,19 @@ def bench_stream(P, torch, S, ev, dev, distinct=2, reps=3):
     for i, b in enumerate(banks):
         st.set_bank(i, b)
     stream = L.stream_ptr(dev)
-    # copies alone (copy stream, host wall clock around a synchronised batch)
+    # copies alone: events on the copy stream around reps * nl stagings
     st.sync_copies()
     torch.cuda.synchronize()
-    t1 = time.perf_counter()
+    cs = st.copy_stream()
+    ce = ev.create(2)
+    ev.record(ce[0], cs)
     for r in range(reps):
         for i in range(nl):
             st._stage((r * nl + i) % 2, i, 0, w.hot)
+    ev.record(ce[1], cs)
     st.sync_copies()
-    copy_ms = (time.perf_counter() - t1) * 1e3 / (reps * nl)
+    copy_ms = ev.ms(ce[0], ce[1]) / (reps * nl)
+    ev.destroy(ce)
     layer_bytes = banks[0].gate.nbytes * 2 + banks[0].down.nbytes
     # compute alone, on resident weights
     W13, W2 = torch.from_numpy(w13).to(dev), torch.from_numpy(w2).to(dev)

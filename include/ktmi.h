@@ -184,6 +184,8 @@ int ktmi_streamer_acquire(ktmi_streamer* s, int slot, void* stream);
 int ktmi_streamer_release(ktmi_streamer* s, int slot, void* stream);
 /* host wait for every copy staged so far */
 int ktmi_streamer_sync(ktmi_streamer* s);
+/* the copy stream (hipStream_t), e.g. to time the copies with events on it */
+void* ktmi_streamer_copy_stream(ktmi_streamer* s);
 /* out[i] = ids[i] - base if base <= ids[i] < base + count, else -1: a group's local slot
  * ids (the reference's `local`, P:40798). */
 int ktmi_remap_ids(const int32_t* ids, int64_t n, int32_t base, int32_t count, int32_t* out, void* stream);

@@ -72,6 +72,7 @@ SIGNATURES = {
     "ktmi_streamer_acquire": (_i32, [_vp, _i32, _vp]),
     "ktmi_streamer_release": (_i32, [_vp, _i32, _vp]),
     "ktmi_streamer_sync": (_i32, [_vp]),
+    "ktmi_streamer_copy_stream": (_vp, [_vp]),
     "ktmi_remap_ids": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp]),
     "ktmi_add_bf16": (_i32, [_vp, _vp, _i64, _vp]),
     "ktmi_host_alloc": (_vp, [_i64]),

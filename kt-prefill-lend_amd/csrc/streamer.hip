@@ -164,6 +164,8 @@ int ktmi_streamer_release(ktmi_streamer* s, int slot, void* stream) {
   return KTMI_OK;
 }
 
+void* ktmi_streamer_copy_stream(ktmi_streamer* s) { return s ? (void*)s->copy : nullptr; }
+
 int ktmi_streamer_sync(ktmi_streamer* s) {
   clear_error();
   KTMI_REQUIRE(s, KTMI_EINVAL, "streamer_sync: null streamer");

@@ -241,6 +241,10 @@ class KTStreamPrefillGGUF:
         self.calls += len(items)
         return outs
 
+    def copy_stream(self) -> int:
+        """The copy stream's handle (hipStream_t as an int)."""
+        return _lib.lib().ktmi_streamer_copy_stream(self._h) or 0
+
     def sync_copies(self):
         _lib.check(_lib.lib().ktmi_streamer_sync(self._h), "streamer_sync")
 
