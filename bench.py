@@ -312,13 +312,16 @@ def bench_stream(P, torch, S, ev, dev, distinct=2, reps=3):
     items = [(i, x, tw_d, slot_d) for i in range(nl)]
     st.run_layers(items)  # warm
     torch.cuda.synchronize()
+    # each pass timed from a drained device, so its first layer's copy overlaps nothing
+    # (back-to-back passes would hide it behind the previous pass's last layer)
     se = ev.create(2)
-    ev.record(se[0], stream)
+    total = 0.0
     for _ in range(reps):
+        ev.record(se[0], stream)
         st.run_layers(items)
-    ev.record(se[1], stream)
-    torch.cuda.synchronize()
-    total = ev.ms(se[0], se[1]) / reps
+        ev.record(se[1], stream)
+        torch.cuda.synchronize()
+        total += ev.ms(se[0], se[1]) / reps
     ev.destroy(se)
     st.close()
     serial = nl * (copy_ms + ms_c)
