@@ -1,11 +1,13 @@
-// B-tile pieces for the grouped MFMA GEMMs: one thread's 32 dequantised weights of one
-// row for one 64-value K step, as 16 packed bf16 words.
+// B pieces for the grouped MFMA GEMMs: one lane's 32 dequantised weights of one row for
+// one 64-value K step, as 16 packed bf16 words.
 //
-// Each format is split into load() (global loads only, into registers) and decode()
-// (ALU only), so a kernel can issue the loads of step k+1 before the MFMAs of step k and
-// decode after them. The values are the exact dequantisation of formats.h rounded once
-// to bf16 (Q4_K uses an FMA: d*sc*q is exact in fp32, so fma(d*sc, q, -dmin*m) rounds the
-// same value as the separate multiply and subtract).
+// Each format is split into load_head() (the bytes a super-block column shares over its
+// four steps: scales, d), load<SUB>() (the step's quant bytes) and decode() (ALU only), so
+// a kernel can keep the loads two steps ahead of their use, load the shared bytes once per
+// super-block, and decode after the MFMAs of the previous step. The values are the exact
+// dequantisation of formats.h rounded once to bf16 (Q4_K uses an FMA: d*sc*q is exact in
+// fp32, so fma(d*sc, q, -dmin*m) rounds the same value as the separate multiply and
+// subtract).
 //
 // K steps: a 256-value super-block column sb is 4 steps SUB = 0..3 of 64 values (SUB is a
 // template parameter: every field position is then a compile-time constant). 256 sb +
@@ -38,29 +40,37 @@ __device__ __forceinline__ const uint32_t* dword_floor(const uint8_t* p) {
 }
 __device__ __forceinline__ uint32_t byte_shift(const uint8_t* p) { return (uint32_t)((uintptr_t)p & 3); }
 
+// a & m where the compiler cannot see the mask, so byte extracts of the result stay
+// single v_cvt_f32_ubyteN conversions instead of folding into bit-field extracts
+__device__ __forceinline__ uint32_t and_opaque(uint32_t a, uint32_t m) {
+  uint32_t r;
+  asm("v_and_b32 %0, %1, %2" : "=v"(r) : "s"(m), "v"(a));
+  return r;
+}
+
 template <int TYPE>
 struct BPiece;
 
 template <>
 struct BPiece<GGML_Q4_K> {
-  struct Raw { u32x4_t hdr, q; };
+  struct Head { u32x4_t hdr; };  // d, dmin, scales[12]
+  struct Raw { u32x4_t q; };
   template <int SUB>
   __device__ static int ksub() { return 64 * SUB; }
   __device__ static int coff(int q) { return 8 * q; }
+  __device__ static void load_head(const uint8_t* row, int sb, int, Head& hd) { hd.hdr = gload<u32x4_t>(row + sb * QB4_K); }
   template <int SUB>
   __device__ static void load(const uint8_t* row, int sb, int h, const uint32_t*, Raw& r) {
-    const uint8_t* b = row + sb * QB4_K;
-    r.hdr = gload<u32x4_t>(b);
-    r.q = gload<u32x4_t>(b + 16 + 32 * SUB + 16 * h);
+    r.q = gload<u32x4_t>(row + sb * QB4_K + 16 + 32 * SUB + 16 * h);
   }
   template <int SUB>
-  __device__ static void decode(const Raw& r, const uint32_t*, uint32_t out[16]) {
-    const float d = half_bits_to_float(r.hdr[0] & 0xFFFF);
-    const float dmin = half_bits_to_float(r.hdr[0] >> 16);
+  __device__ static void decode(const Head& hd, const Raw& r, const uint32_t*, uint32_t out[16]) {
+    const float d = half_bits_to_float(hd.hdr[0] & 0xFFFF);
+    const float dmin = half_bits_to_float(hd.hdr[0] >> 16);
     // sub-blocks 2g, 2g+1: for g < 2 the 6-bit fields sit in scales[0..7]; for g >= 2 the
     // low 4 bits are in scales[8..11] and the high 2 bits in bits 6-7 of scales[0..7]
     constexpr int sh = 16 * (SUB & 1);
-    const uint32_t ws = r.hdr[1] >> sh, wm = r.hdr[2] >> sh, lo = r.hdr[3] >> sh;
+    const uint32_t ws = hd.hdr[1] >> sh, wm = hd.hdr[2] >> sh, lo = hd.hdr[3] >> sh;
     constexpr bool hi = SUB >= 2;
     const int sc0 = hi ? (int)((lo & 15) | (((ws >> 6) & 3) << 4)) : (int)(ws & 63);
     const int sc1 = hi ? (int)(((lo >> 8) & 15) | (((ws >> 14) & 3) << 4)) : (int)((ws >> 8) & 63);
@@ -68,13 +78,15 @@ struct BPiece<GGML_Q4_K> {
     const int m1 = hi ? (int)(((lo >> 12) & 15) | (((wm >> 14) & 3) << 4)) : (int)((wm >> 8) & 63);
     const float d1a = d * (float)sc0, m1a = dmin * (float)m0;
     const float d1b = d * (float)sc1, m1b = dmin * (float)m1;
+    // 4 bytes = 4 low nibbles (positions off0..) and 4 high nibbles (off1..); each nibble
+    // masked into its own byte converts with one v_cvt_f32_ubyteN
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t w = r.q[i >> 1] >> (16 * (i & 1));
-      const float l0 = (float)(w & 15), l1 = (float)((w >> 8) & 15);
-      const float h0 = (float)((w >> 4) & 15), h1 = (float)((w >> 12) & 15);
-      out[i] = f2bf2(__builtin_fmaf(d1a, l0, -m1a), __builtin_fmaf(d1a, l1, -m1a));
-      out[8 + i] = f2bf2(__builtin_fmaf(d1b, h0, -m1b), __builtin_fmaf(d1b, h1, -m1b));
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t nl = and_opaque(r.q[i], 0x0F0F0F0Fu), nh = and_opaque(r.q[i] >> 4, 0x0F0F0F0Fu);
+      out[2 * i] = f2bf2(__builtin_fmaf(d1a, (float)(nl & 0xFF), -m1a), __builtin_fmaf(d1a, (float)((nl >> 8) & 0xFF), -m1a));
+      out[2 * i + 1] = f2bf2(__builtin_fmaf(d1a, (float)((nl >> 16) & 0xFF), -m1a), __builtin_fmaf(d1a, (float)(nl >> 24), -m1a));
+      out[8 + 2 * i] = f2bf2(__builtin_fmaf(d1b, (float)(nh & 0xFF), -m1b), __builtin_fmaf(d1b, (float)((nh >> 8) & 0xFF), -m1b));
+      out[8 + 2 * i + 1] = f2bf2(__builtin_fmaf(d1b, (float)((nh >> 16) & 0xFF), -m1b), __builtin_fmaf(d1b, (float)(nh >> 24), -m1b));
     }
   }
   __device__ static int off0(int h) { return 16 * h; }
@@ -83,10 +95,12 @@ struct BPiece<GGML_Q4_K> {
 
 template <>
 struct BPiece<GGML_Q8_0> {
+  struct Head {};
   struct Raw { uint32_t w[9]; uint32_t s; };
   template <int SUB>
   __device__ static int ksub() { return 64 * SUB; }
   __device__ static int coff(int q) { return 8 * q; }
+  __device__ static void load_head(const uint8_t*, int, int, Head&) {}
   template <int SUB>
   __device__ static void load(const uint8_t* row, int sb, int h, const uint32_t*, Raw& r) {
     const uint8_t* b = row + (8 * sb + 2 * SUB + h) * QB8_0;
@@ -101,7 +115,7 @@ struct BPiece<GGML_Q8_0> {
     r.w[8] = gload<uint32_t>(a + 8);
   }
   template <int SUB>
-  __device__ static void decode(const Raw& r, const uint32_t*, uint32_t out[16]) {
+  __device__ static void decode(const Head&, const Raw& r, const uint32_t*, uint32_t out[16]) {
     const float d = half_bits_to_float(r.s ? (r.w[0] >> 16) : (r.w[0] & 0xFFFF));
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -118,15 +132,25 @@ struct BPiece<GGML_Q8_0> {
 
 template <>
 struct BPiece<GGML_Q6_K> {
-  struct Raw { uint32_t ql[5], qh[5], sw0, sw1, dw; uint32_t s; uint32_t sp; };
+  // the 20 bytes from the dword below scales[0]: scales[16] and d, s = byte shift
+  struct Head { uint32_t w[5]; uint32_t s; };
+  struct Raw { uint32_t ql[5], qh[5]; };
   template <int SUB>
   __device__ static int ksub() { return 128 * (SUB >> 1) + 32 * (SUB & 1); }
   __device__ static int coff(int q) { return q < 4 ? 8 * q : 64 + 8 * (q - 4); }
+  __device__ static void load_head(const uint8_t* row, int sb, int, Head& hd) {
+    const uint8_t* sc = row + sb * QB6_K + 192;
+    hd.s = byte_shift(sc);
+    const uint32_t* a = dword_floor(sc);
+    const u32x4_t w = gload<u32x4_a4_t>(a);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hd.w[i] = w[i];
+    hd.w[4] = gload<uint32_t>(a + 4);
+  }
   template <int SUB>
   __device__ static void load(const uint8_t* row, int sb, int h, const uint32_t*, Raw& r) {
     const uint8_t* b = row + sb * QB6_K;
     constexpr int hh = SUB >> 1, c = SUB & 1;
-    r.s = byte_shift(b);
     const uint32_t* ql = dword_floor(b + 64 * hh + 32 * c + 16 * h);
     const uint32_t* qh = dword_floor(b + 128 + 32 * hh + 16 * h);
     // 16 bytes each from the dword below them: one dwordx4 and the dword after it
@@ -138,25 +162,24 @@ struct BPiece<GGML_Q6_K> {
     }
     r.ql[4] = gload<uint32_t>(ql + 4);
     r.qh[4] = gload<uint32_t>(qh + 4);
-    // scales[8hh + 2c + h] and scales[8hh + 2c + h + 4] (run c+2) lie in the 8 bytes from
-    // the dword below the first
-    const uint8_t* sc = b + 192 + 8 * hh + 2 * c + h;
-    r.sp = 8 * byte_shift(sc);
-    const u32x2_t s2 = gload<u32x2_a4_t>(dword_floor(sc));
-    r.sw0 = s2[0];
-    r.sw1 = s2[1];
-    r.dw = gload<uint32_t>(dword_floor(b + 208));
   }
   template <int SUB>
-  __device__ static void decode(const Raw& r, const uint32_t*, uint32_t out[16]) {
-    const float d = half_bits_to_float(r.s ? (r.dw >> 16) : (r.dw & 0xFFFF));
-    const float d1a = d * (float)(int8_t)((r.sw0 >> r.sp) & 0xFF);
-    const float d1b = d * (float)(int8_t)((r.sw1 >> r.sp) & 0xFF);
-    constexpr int hsh = 2 * (SUB & 1);
+  __device__ static void decode(const Head& hd, const Raw& r, const uint32_t*, uint32_t out[16]) {
+    constexpr int hh = SUB >> 1, c = SUB & 1;
+    const uint32_t s = hd.s;  // the same shift as the block start (192 = 0 mod 4)
+    // scales[8hh + 2c + h] (run c) and scales[8hh + 2c + h + 4] (run c+2): bytes 2c + h of
+    // the realigned scale words 2hh and 2hh + 1
+    const uint32_t h8 = 8 * ((threadIdx.x >> 5) & 1);
+    const uint32_t sa = alignbyte(hd.w[2 * hh + 1], hd.w[2 * hh], s);
+    const uint32_t sbw = alignbyte(hd.w[2 * hh + 2], hd.w[2 * hh + 1], s);
+    const float d = half_bits_to_float(alignbyte(hd.w[4], hd.w[4], s) & 0xFFFF);
+    const float d1a = d * (float)(int8_t)((sa >> (16 * c + h8)) & 0xFF);
+    const float d1b = d * (float)(int8_t)((sbw >> (16 * c + h8)) & 0xFF);
+    constexpr int hsh = 2 * c;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t lw = alignbyte(r.ql[i + 1], r.ql[i], r.s);
-      const uint32_t hw = alignbyte(r.qh[i + 1], r.qh[i], r.s);
+      const uint32_t lw = alignbyte(r.ql[i + 1], r.ql[i], s);
+      const uint32_t hw = alignbyte(r.qh[i + 1], r.qh[i], s);
       const uint32_t va = (lw & 0x0F0F0F0Fu) | (((hw >> hsh) & 0x03030303u) << 4);
       const uint32_t vb = ((lw >> 4) & 0x0F0F0F0Fu) | (((hw >> (hsh + 4)) & 0x03030303u) << 4);
       out[2 * i] = f2bf2(d1a * (float)((int)(va & 0xFF) - 32), d1a * (float)((int)((va >> 8) & 0xFF) - 32));
@@ -171,37 +194,62 @@ struct BPiece<GGML_Q6_K> {
 
 template <>
 struct BPiece<GGML_IQ3_S> {
-  struct Raw { uint32_t qs0, qs1, sg, misc; };  // misc: d | qh << 16 | scale nibble << 24
+  // d and the 4 scale bytes of the block (dwords below them, realigned at decode)
+  struct Head { uint32_t dw, sc0, sc1; uint32_t s; };
+  // qs[8] of group ib (3 dwords from below), qh byte's dword, signs[4] (2 dwords from below)
+  struct Raw { uint32_t qs[3], sg[2], qh; };
   template <int SUB>
   __device__ static int ksub() { return 64 * SUB; }
   __device__ static int coff(int q) { return 8 * q; }
+  __device__ static void load_head(const uint8_t* row, int sb, int, Head& hd) {
+    const uint8_t* b = row + sb * QBIQ3_S;
+    hd.s = byte_shift(b);
+    hd.dw = gload<uint32_t>(dword_floor(b));
+    hd.sc0 = gload<uint32_t>(dword_floor(b + 106));
+    hd.sc1 = gload<uint32_t>(dword_floor(b + 108));
+  }
   template <int SUB>
   __device__ static void load(const uint8_t* row, int sb, int h, const uint32_t*, Raw& r) {
     const uint8_t* b = row + sb * QBIQ3_S;
     const int ib = 2 * SUB + h;
-    r.qs0 = ld_u32_a2(b + 2 + 8 * ib);
-    r.qs1 = ld_u32_a2(b + 6 + 8 * ib);
-    r.sg = ld_u32_a2(b + 74 + 4 * ib);
-    const uint32_t nib = (gload<uint8_t>(b + 106 + ib / 2) >> (4 * (ib & 1))) & 15;
-    r.misc = (uint32_t)ld_u16(b) | ((uint32_t)gload<uint8_t>(b + 66 + ib) << 16) | (nib << 24);
+    const uint32_t* q = dword_floor(b + 2 + 8 * ib);
+    const u32x2_t q2 = gload<u32x2_a4_t>(q);
+    r.qs[0] = q2[0];
+    r.qs[1] = q2[1];
+    r.qs[2] = gload<uint32_t>(q + 2);
+    const u32x2_t s2 = gload<u32x2_a4_t>(dword_floor(b + 74 + 4 * ib));
+    r.sg[0] = s2[0];
+    r.sg[1] = s2[1];
+    r.qh = gload<uint32_t>(dword_floor(b + 66 + ib));
   }
   template <int SUB>
-  __device__ static void decode(const Raw& r, const uint32_t* grid, uint32_t out[16]) {
-    const float db = half_bits_to_float(r.misc & 0xFFFF) * (float)(1 + 2 * (int)(r.misc >> 24));
-    const uint32_t qh = (r.misc >> 16) & 0xFF;
+  __device__ static void decode(const Head& hd, const Raw& r, const uint32_t* grid, uint32_t out[16]) {
+    const uint32_t s = hd.s;
+    const uint32_t h = (threadIdx.x >> 5) & 1;
+    const int ib = 2 * SUB + (int)h;
+    // block byte offsets: qs at 2 + 8 ib, signs at 74 + 4 ib (both = s + 2 mod 4),
+    // qh at 66 + ib, scales at 106, d at 0
+    const uint32_t s2 = (s + 2) & 3;
+    const uint32_t qs0 = alignbyte(r.qs[1], r.qs[0], s2), qs1 = alignbyte(r.qs[2], r.qs[1], s2);
+    const uint32_t sg = alignbyte(r.sg[1], r.sg[0], s2);
+    const uint32_t qh = (r.qh >> (8 * ((s + 2 + ib) & 3))) & 0xFF;
+    const uint32_t scw = alignbyte(hd.sc1, hd.sc0, s2);  // scales[0..3]
+    const uint32_t nib = (scw >> (8 * (ib >> 1) + 4 * (ib & 1))) & 15;
+    const uint32_t dbits = (hd.dw >> (8 * s)) & 0xFFFF;
+    const float db = half_bits_to_float(dbits) * (float)(1 + 2 * (int)nib);
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
-      const uint32_t sb = (r.sg >> (8 * l)) & 0xFF;
+      const uint32_t sbits = (sg >> (8 * l)) & 0xFF;
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
         const int k = 2 * l + sub;
-        const uint32_t qsb = ((k < 4 ? r.qs0 : r.qs1) >> (8 * (k & 3))) & 0xFF;
+        const uint32_t qsb = ((k < 4 ? qs0 : qs1) >> (8 * (k & 3))) & 0xFF;
         const uint32_t g = grid[qsb | (((qh >> k) & 1) << 8)];
         float y[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const float v = db * (float)((g >> (8 * j)) & 0xFF);
-          y[j] = ((sb >> (4 * sub + j)) & 1) ? -v : v;
+          y[j] = ((sbits >> (4 * sub + j)) & 1) ? -v : v;
         }
         out[2 * k] = f2bf2(y[0], y[1]);
         out[2 * k + 1] = f2bf2(y[2], y[3]);

@@ -6,8 +6,9 @@
 //      every route's position is a pure function of the ids: no host sync, no atomics
 //      on positions, graph-capturable.
 //   2. gemm<GATEUP>: for each (slot, tile of BM sorted routes, tile of N) the gathered
-//      bf16 rows of x times the slot's gate and up rows, dequantised from raw GGUF blocks
-//      into LDS (bf16, RNE of the exact fp32 dequant value), on
+//      bf16 rows of x (staged in LDS by direct buffer->LDS loads) times the slot's gate and
+//      up rows, which each lane dequantises from raw GGUF blocks straight into its MFMA
+//      operand registers (bf16, RNE of the exact fp32 dequant value), on
 //      v_mfma_f32_32x32x16_bf16; the epilogue applies silu(gate)*up and writes bf16 rows
 //      of H in sorted order.
 //   3. gemm<down>: H rows (contiguous in sorted order) times the slot's down rows; the
@@ -31,32 +32,27 @@ constexpr int CHW = 256;         // routes per wave chunk in the sort
 constexpr int SORT_THREADS = 256;
 constexpr int MAX_SLOTS = 512;
 
-// tile configuration: 8 waves in 2 (M) x 4 (N), each 128 routes x 64 weight rows (8
-// accumulators of 32 x 32, two waves per SIMD); tile = 256 routes x 256 weight rows
-// (GATEUP: 128 gate + 128 up rows)
+// tile configuration: 4 waves (one per SIMD); wave w owns FI fragments of 32 weight rows
+// and all FJ fragments of 32 routes of the tile: FI x FJ = 16 accumulators of 32 x 32
+// (256 accumulation registers per lane). Tile = BNW weight rows x BM routes (GATEUP: the
+// wave's first FI/2 fragments are gate rows, the others the up rows of the same columns).
+// The weights never touch LDS: each lane loads the raw GGUF bytes of its FI rows and
+// decodes them straight into MFMA operand registers; LDS holds only the activation tile.
 constexpr int BK = 64;
-constexpr int FM = 4, FN = 2, WM = 2, WN = 4;
-constexpr int NTHREADS = WM * WN * 64;
-constexpr int NWAVES = WM * WN;
-constexpr int BM = WM * FM * 32;   // routes per tile
-constexpr int BNW = WN * FN * 32;  // weight rows per tile
-constexpr int PIECES = 2 * BNW / NTHREADS;  // 32-value B pieces per thread per step
-// LDS: the A tile in ADEPTH buffers (activations prefetched ADEPTH-1 steps ahead by direct
-// global->LDS loads), the B tile (decoded weights) in 2 buffers; rows of 128 B in both,
-// 16-byte slots swizzled (see lds_slot); 3 + 2 buffers fill the 160 KB of LDS, so the
-// IQ3_S kernels (2 KB codebook in LDS) use 2 A buffers.
-constexpr int A_BYTES = BM * BK * 2;
-constexpr int B_BYTES = BNW * BK * 2;
-constexpr int CPITCH_UP = BNW / 2 + 8;  // epilogue C tile pitches (bf16 elements)
-constexpr int CPITCH_DN = BNW + 8;
-constexpr int SMEM_C = BM * CPITCH_DN * 2;
-template <int TYPE>
-constexpr int adepth() { return TYPE == GGML_IQ3_S ? 2 : 3; }
-template <int TYPE>
-constexpr int smem_bytes() {
-  return adepth<TYPE>() * A_BYTES + 2 * B_BYTES > SMEM_C ? adepth<TYPE>() * A_BYTES + 2 * B_BYTES : SMEM_C;
-}
-static_assert(3 * A_BYTES + 2 * B_BYTES <= 160 * 1024, "LDS");
+constexpr int WN = 4, WM = 1;          // waves over weight rows x waves over routes
+constexpr int NWAVES = WN * WM;
+constexpr int NTHREADS = NWAVES * 64;
+constexpr int FI = 2, FJ = 8;
+constexpr int BNW = WN * FI * 32;      // weight rows per tile
+constexpr int BM = WM * FJ * 32;       // routes per tile
+constexpr int A_ROW = BK * 2;          // bytes of one activation row per K step
+constexpr int A_BYTES = BM * A_ROW;
+// activation buffers: steps k .. k+AD-1 in flight (direct global->LDS loads AD-1 steps
+// ahead); rows of 128 B, 16-byte slots swizzled (lds_slot)
+constexpr int AD = 4;
+constexpr int AJ = A_BYTES / (16 * NTHREADS);  // direct loads per thread per step
+static_assert(AD * A_BYTES + 2048 <= 160 * 1024, "LDS");
+static_assert(AJ % 2 == 0, "A loads are spread over the 2 regions of a step");
 
 // ---- route sort by slot. hist is slot-major: hist[e * nch + chunk].
 
@@ -119,10 +115,12 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_scan_chunks(int32_t* __rest
   if (threadIdx.x == 0) tot[blockIdx.x] = total;
 }
 
-// one block: seg[S+1] (route offsets) and tseg[S+1] (tile offsets, tiles of bm routes)
+// one block: seg[S+1] (route offsets), tseg[S+1] (tile offsets, tiles of bm routes) and
+// tile_slot[tile] (the slot of each tile)
 __global__ __launch_bounds__(SORT_THREADS) void sort_scan_slots(const int32_t* __restrict__ tot, int S,
                                                                 int32_t* __restrict__ seg,
-                                                                int32_t* __restrict__ tseg, int bm) {
+                                                                int32_t* __restrict__ tseg,
+                                                                int32_t* __restrict__ tile_slot, int bm) {
   __shared__ int buf[SORT_THREADS];
   const int t = threadIdx.x;
   // two slots per thread (S <= 512)
@@ -136,6 +134,8 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_scan_slots(const int32_t* _
   if (e0 < S) { seg[e0] = ea; tseg[e0] = eb; }
   if (e1 < S) { seg[e1] = ea + a0; tseg[e1] = eb + b0; }
   if (t == 0) { seg[S] = ta; tseg[S] = tb; }
+  for (int q = 0; q < b0; ++q) tile_slot[eb + q] = e0;
+  for (int q = 0; q < b1; ++q) tile_slot[eb + b0 + q] = e1;
 }
 
 __global__ __launch_bounds__(SORT_THREADS) void sort_scatter(const int32_t* __restrict__ slot_ids, int64_t R, int S,
@@ -180,80 +180,84 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_scatter(const int32_t* __re
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + __expf(-g)) * u; }
 
-// GATEUP = true : A = x rows gathered through perm (token = p / top_k), Kdim = hidden,
-//                 B rows = [gate n0..n0+BNW/2 ; up NI+n0..], out = H [R, NI] sorted rows.
-// GATEUP = false: A = H rows m0.., Kdim = inter, B rows = down rows c0..c0+BNW,
-//                 out = Y [routes, NI] at row perm[m] (NI = hidden).
-//
-// K loop over 64-value steps (bpiece.h maps step positions to row offsets), one barrier
-// per step. Step k: load the raw B bytes of step k+2 into a register ring; MFMAs of step k
-// from the A buffer k % AD and B buffer k & 1, with the decode of B(k+1) (raw bytes loaded
-// a step earlier) into the other B buffer in the same basic block, so the scheduler can
-// interleave the decode VALU with the matrix core, and the direct global->LDS loads of
-// A(k+AD-1) spread over the sub-steps; wait for A(k+1) and the B stores; barrier.
-// Loads past the last step re-read the last step (clamped, unused), keeping the loop
-// branch-free.
-// Workgroup barrier for the K loop. The caller has already waited for its own LDS writes
-// (s_waitcnt): __syncthreads() would add a workgroup fence that also waits for every
-// outstanding direct global->LDS load, including the ones meant to stay in flight. The
-// wavefront-scope fences only keep the compiler from moving memory operations across.
+// Workgroup barrier for the K loop. The caller has already waited for its own LDS traffic:
+// __syncthreads() would add a workgroup fence that also waits for every outstanding direct
+// global->LDS load, including the ones meant to stay in flight. The wavefront-scope fences
+// only keep the compiler from moving memory operations across.
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// A and B rows are 128 B in LDS; the 16-byte slot of chunk c of row r is
-// c ^ (r & 7) ^ ((r >> 3) & 1): any 8 consecutive rows use 8 different slots (no conflict
-// with 32 four-byte banks) and any 16 consecutive rows 16 different (row parity, slot)
-// pairs (no conflict with 64 banks), for the 32-row MFMA operand reads.
+// s_waitcnt operand that waits until at most n vector memory operations are outstanding
+// (vmcnt bits 3:0 and 15:14; expcnt 7 and lgkmcnt 15 mean no wait on those counters)
+constexpr int wait_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// Activation rows are 128 B in LDS; the 16-byte slot of chunk c of row r is
+// c ^ (r & 7) ^ ((r >> 3) & 1): any 8 consecutive rows use 8 different slots and any 16
+// consecutive rows 16 different (row parity, slot) pairs, so the 32-row MFMA operand reads
+// are free of bank conflicts.
 __device__ __forceinline__ int lds_slot(int row, int chunk) { return chunk ^ (row & 7) ^ ((row >> 3) & 1); }
 
+// GATEUP = true : activations = x rows gathered through perm (token = p / top_k),
+//                 Kdim = hidden, weight rows = [gate n0.. ; up NI+n0..], out = H [R, NI]
+//                 sorted rows, silu(gate) * up.
+// GATEUP = false: activations = H rows m0.., Kdim = inter, weight rows = down rows of the
+//                 tile's columns, out = Y [routes, NI] at row perm[m] (NI = hidden).
+//
+// MFMA operands: srcA = weights (row = lane % 32 of a 32-row fragment), srcB = activations
+// (column = route lane % 32); k = 8 (lane / 32) + [0, 8) of each 16-value sub-step. The
+// K positions a lane covers in a 64-value step are those of its decoded piece (bpiece.h:
+// half h = lane / 32 of the step, 16 values at off0(h) and 16 at off1(h)); sub-step s
+// takes the piece's values 8s..8s+7, and reads the activation chunk at the same positions.
+//
+// K loop, step k (one barrier per step): raw weight bytes of step k+2 into a register ring
+// (and, once per super-block column, the next column's scales into head_nxt); 4 sub-steps
+// of FI x FJ MFMAs on the weights decoded one step earlier and the activation buffer
+// k % AD, with the decode of step k+1 and the direct loads of activation step k+AD-1
+// spread over the sub-steps. Loads past the last step re-read the last one (clamped,
+// unused), keeping the loop branch-free.
+//
+// Epilogue: the accumulators are converted (GATEUP: silu(gate) * up) into a bf16 C tile
+// in LDS, then written out as whole rows.
 template <int TYPE, bool GATEUP>
-__global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restrict__ A_src,
+__global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes,
                                                          const int32_t* __restrict__ perm,
                                                          const int32_t* __restrict__ seg,
-                                                         const int32_t* __restrict__ tseg, int S, int top_k,
+                                                         const int32_t* __restrict__ tseg,
+                                                         const int32_t* __restrict__ tile_slot, int S, int top_k,
                                                          const uint8_t* __restrict__ W, int w_is_table,
                                                          int64_t w_expert_stride, int64_t rb, int Kdim, int NI,
                                                          int NT, int64_t nblk, uint16_t* __restrict__ out) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[smem_bytes<TYPE>()];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[AD * A_BYTES];
   __shared__ uint32_t grid_lds[TYPE == GGML_IQ3_S ? 512 : 1];
   using BP = BPiece<TYPE>;
 
   // XCD-aware order: workgroups are dealt to the 8 XCDs round-robin (pid % 8). All NT
-  // N tiles of one M tile go to the same XCD, so they share its L2 for the gathered A
-  // rows; M tiles rotate over the XCDs, so the real tiles (a prefix of the M range, the
-  // rest exit at once) spread evenly. gridDim.x is a multiple of 8 * NT.
+  // N tiles of one M tile go to the same XCD, so they share its L2 for the gathered
+  // activation rows; M tiles rotate over the XCDs. gridDim.x is a multiple of 8 * NT.
   const int64_t pid = blockIdx.x;
   const int64_t idx = pid >> 3;
   const int mt = (int)((idx / NT) * 8 + (pid & 7));
   const int nt = (int)(idx % NT);
   if ((int64_t)mt * NT + nt >= nblk) return;
-  const int total_tiles = tseg[S];
-  if (mt >= total_tiles) return;
-  int lo = 0, hi = S;
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if (tseg[mid] <= mt) lo = mid; else hi = mid;
-  }
-  const int e = lo;
+  if (mt >= tseg[S]) return;
+  const int e = tile_slot[mt];
   const int m0 = seg[e] + (mt - tseg[e]) * BM;
   const int valid = min(BM, seg[e + 1] - m0);
 
   if constexpr (TYPE == GGML_IQ3_S) stage_iq3s_grid(grid_lds);
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave % WN, wm = wave / WN;
+  const int h = lane >> 5, l32 = lane & 31;
   const uint8_t* wexp = w_is_table ? (const uint8_t*)((const int64_t*)W)[e] : W + (int64_t)e * w_expert_stride;
-  constexpr int AD = adepth<TYPE>();
-  uint8_t* Abuf0 = smem;
-  uint8_t* Bbuf0 = smem + AD * A_BYTES;
 
-  // ---- A sources: direct loads, instruction j of wave w fills rows 8*(NWAVES*j + w) + lane/8
-  constexpr int AJ = BM / (8 * NWAVES);
-  int a_off[AJ];  // element offset of this lane's 16-byte chunk, without the step base
+  // ---- activation sources: direct loads, instruction j of wave w fills rows
+  // 8 * (NWAVES * j + w) + lane / 8, LDS slot lane % 8
+  uint32_t a_off[AJ];  // byte offset of this lane's 16-byte chunk, without the step base
 #pragma unroll
   for (int j = 0; j < AJ; ++j) {
     const int row = 8 * (NWAVES * j + wave) + (lane >> 3);
@@ -262,60 +266,60 @@ __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restr
     int src_row;
     if constexpr (GATEUP) src_row = perm[m0 + r] / top_k;
     else src_row = m0 + r;
-    a_off[j] = src_row * Kdim + BP::coff(chunk);
+    a_off[j] = 2u * (uint32_t)(src_row * Kdim + BP::coff(chunk));
   }
-  auto issue_a = [&](int sb, auto subc, int buf, int j0 = 0, int j1 = AJ) {
+  // buffer loads into LDS: the step's column offset is a scalar operand, the lane's row
+  // offset a fixed register, so no address arithmetic per load; reads beyond a_bytes
+  // (never made: rows are clamped to the tile's last valid one) would return zeros
+  const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)A_src, (short)0, a_bytes, 0x00020000);
+  auto issue_a = [&](int sb, auto subc, int buf, int j0, int j1) {
     constexpr int SUB = decltype(subc)::value;
-    const int kb = 256 * sb + BP::template ksub<SUB>();
+    const int sbase = 2 * (256 * sb + BP::template ksub<SUB>());
 #pragma unroll
     for (int j = j0; j < j1; ++j) {
-      uint8_t* dst = Abuf0 + buf * A_BYTES + (8 * (NWAVES * j + wave)) * (BK * 2);
-      __builtin_amdgcn_global_load_lds(A_src + a_off[j] + kb, dst, 16, 0, 0);
+      uint8_t* dst = smem + buf * A_BYTES + (8 * (NWAVES * j + wave)) * A_ROW;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (__attribute__((address_space(3))) void*)dst, 16, (int)a_off[j],
+                                               sbase, 0, 0);
     }
   };
 
-  // ---- B source: piece p of thread t is half (q & 1) of weight row q >> 1, q = t * PIECES + p
-  const uint8_t* b_row[PIECES];
-  int b_j[PIECES], b_h[PIECES];
+  // ---- this lane's weight rows: row l32 of each of the wave's FI fragments
+  const uint8_t* b_row[FI];
 #pragma unroll
-  for (int p = 0; p < PIECES; ++p) {
-    const int q = tid * PIECES + p;
-    b_j[p] = q >> 1;
-    b_h[p] = q & 1;
+  for (int i = 0; i < FI; ++i) {
     int64_t wr;
     if constexpr (GATEUP) {
-      const int half = BNW / 2;
-      const int n0 = nt * half;
-      wr = b_j[p] < half ? (n0 + b_j[p]) : (NI + n0 + (b_j[p] - half));
+      constexpr int FH = FI / 2;
+      const int n0 = nt * (BNW / 2);
+      wr = i < FH ? (int64_t)n0 + (wn * FH + i) * 32 + l32 : (int64_t)NI + n0 + (wn * FH + i - FH) * 32 + l32;
     } else {
-      wr = (int64_t)nt * BNW + b_j[p];
+      wr = (int64_t)nt * BNW + (wn * FI + i) * 32 + l32;
     }
-    b_row[p] = wexp + wr * rb;
+    b_row[i] = wexp + wr * rb;
   }
-  auto store_b = [&](const uint32_t* breg, int p, int buf) {
-    uint8_t* bd = Bbuf0 + buf * B_BYTES + b_j[p] * (BK * 2);
-    const int c0 = BP::off0(b_h[p]) / 8, c1 = BP::off1(b_h[p]) / 8;
-    u32x4_t v0 = {breg[0], breg[1], breg[2], breg[3]};
-    u32x4_t v1 = {breg[4], breg[5], breg[6], breg[7]};
-    u32x4_t v2 = {breg[8], breg[9], breg[10], breg[11]};
-    u32x4_t v3 = {breg[12], breg[13], breg[14], breg[15]};
-    *(u32x4_t*)(bd + 16 * lds_slot(b_j[p], c0)) = v0;
-    *(u32x4_t*)(bd + 16 * lds_slot(b_j[p], c0 + 1)) = v1;
-    *(u32x4_t*)(bd + 16 * lds_slot(b_j[p], c1)) = v2;
-    *(u32x4_t*)(bd + 16 * lds_slot(b_j[p], c1 + 1)) = v3;
-  };
 
-  f32x16_t acc[FM][FN];
+  // LDS byte offset of this lane's activation operand in sub-step s for route fragment 0
+  // (fragment j adds 32 rows; the slot depends on the row's low 4 bits only)
+  int a_rd[4];
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+  for (int s = 0; s < 4; ++s) {
+    const int q = s < 2 ? BP::off0(h) / 8 + s : BP::off1(h) / 8 + s - 2;
+    a_rd[s] = (wm * FJ * 32 + l32) * A_ROW + 16 * lds_slot(l32, q);
+  }
+
+  f32x16_t acc[FI][FJ];
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
+  for (int i = 0; i < FI; ++i)
+#pragma unroll
+    for (int j = 0; j < FJ; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // raw ring: slot (k & 1) holds the bytes of step k (loaded two steps ahead)
-  typename BP::Raw raw[2][PIECES];
-  uint32_t breg[16];
+  // raw ring: slot (k & 1) holds the bytes of step k (loaded two steps ahead); wv[k & 1]
+  // the decoded weights of step k (decoded one step ahead)
+  typename BP::Raw raw[2][FI];
+  typename BP::Head head[FI], head_nxt[FI];  // super-block sb's shared bytes, and sb+1's
+  uint32_t wv[2][FI][16];
   const int nsb = Kdim / 256;  // super-block columns, 4 steps each
   const int lsb = nsb - 1;
   using S0 = std::integral_constant<int, 0>;
@@ -323,96 +327,97 @@ __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restr
   using S2 = std::integral_constant<int, 2>;
   using S3 = std::integral_constant<int, 3>;
 
-  if constexpr (TYPE == GGML_IQ3_S) __syncthreads();
-  issue_a(0, S0{}, 0);
-  if constexpr (AD == 3) issue_a(0, S1{}, 1);
+  // prologue: raw(0), raw(1), A(0), A(1), A(2); then wait for A(0) only (the newest
+  // 2 AJ loads stay in flight), which also covers the raw bytes, and decode step 0
 #pragma unroll
-  for (int p = 0; p < PIECES; ++p) {
-    BP::template load<0>(b_row[p], 0, b_h[p], grid_lds, raw[0][p]);
-    BP::template load<1>(b_row[p], 0, b_h[p], grid_lds, raw[1][p]);
-  }
+  for (int i = 0; i < FI; ++i) BP::load_head(b_row[i], 0, h, head[i]);
 #pragma unroll
-  for (int p = 0; p < PIECES; ++p) {
-    BP::template decode<0>(raw[0][p], grid_lds, breg);
-    store_b(breg, p, 0);
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
+  for (int i = 0; i < FI; ++i) BP::template load<0>(b_row[i], 0, h, grid_lds, raw[0][i]);
+#pragma unroll
+  for (int i = 0; i < FI; ++i) BP::template load<1>(b_row[i], 0, h, grid_lds, raw[1][i]);
+  issue_a(0, S0{}, 0, 0, AJ);
+  issue_a(0, S1{}, 1, 0, AJ);
+  issue_a(0, S2{}, 2, 0, AJ);
+  static_assert(2 * AJ < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(wait_vmcnt(2 * AJ));
+  __syncthreads();  // A(0) of every wave; the codebook
+#pragma unroll
+  for (int i = 0; i < FI; ++i) BP::template decode<0>(head[i], raw[0][i], grid_lds, wv[0][i]);
 
-  // step SUB of super-block column sb (step k = 4 sb + SUB); the B buffer parity and the
-  // raw ring slot are SUB & 1, the A buffer is k % AD (abuf). Loads beyond the last step
-  // re-read the last column (in bounds, unused), so the body has no branches.
   int abuf = 0;
   auto step = [&](int sb, auto subc) {
     constexpr int SUB = decltype(subc)::value;
-    constexpr int buf = SUB & 1;
-    constexpr int SUB1 = (SUB + 1) & 3, SUB2 = (SUB + 2) & 3;
-    constexpr int SUBA = (SUB + AD - 1) & 3;  // step k + AD - 1
+    constexpr int cur = SUB & 1;
+    constexpr int SUB1 = (SUB + 1) & 3, SUB2 = (SUB + 2) & 3, SUB3 = (SUB + 3) & 3;
     const int sb2 = SUB < 2 ? sb : min(sb + 1, lsb);
-    const int sba = SUB + AD - 1 < 4 ? sb : min(sb + 1, lsb);
-    // raw bytes of step k+2 replace those of step k (decoded one step ago), then the A
-    // tile of step k+AD-1: the A loads are the newest VMEM, so the wait below can leave
-    // just them in flight
+    const int sb3 = SUB < 1 ? sb : min(sb + 1, lsb);
 #pragma unroll
-    for (int p = 0; p < PIECES; ++p) BP::template load<SUB2>(b_row[p], sb2, b_h[p], grid_lds, raw[buf][p]);
+    for (int i = 0; i < FI; ++i) BP::template load<SUB2>(b_row[i], sb2, h, grid_lds, raw[cur][i]);
+    if constexpr (SUB == 1) {
+#pragma unroll
+      for (int i = 0; i < FI; ++i) BP::load_head(b_row[i], min(sb + 1, lsb), h, head_nxt[i]);
+    }
     int anext = abuf + AD - 1;
     if (anext >= AD) anext -= AD;
-    const uint8_t* Ab = Abuf0 + abuf * A_BYTES;
-    const uint8_t* Bb = Bbuf0 + buf * B_BYTES;
+    const uint8_t* Ab = smem + abuf * A_BYTES;
+    // two regions of two sub-steps; in each: 4 of the direct loads of A(k+3), the reads
+    // of the next sub-steps' activation operands (double-buffered in registers), 32 MFMAs
+    // and one piece of the decode of step k+1, interleaved by the schedule below so the
+    // matrix core never waits for a run of decode or for an LDS read
+    static_assert(FI == 2, "the schedule assumes 2 pieces per step");
+    constexpr int NMR = 2 * FI * FJ;       // MFMAs per region
+    constexpr int DSR = NMR / (2 * FJ);    // MFMAs per LDS read
+    bf16x8_t af[2][FJ];
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += 16) {
-      // the A loads of step k+AD-1 go out over the last three MFMA sub-steps: the waves
-      // leave the barrier together, and one burst of every wave's loads would queue them
-      // behind each other at the address unit
-      if (kk >= 16) {
-        constexpr int NPART = 3;
-        const int part = kk / 16 - 1;
-        __builtin_amdgcn_sched_barrier(0);
-        issue_a(sba, std::integral_constant<int, SUBA>{}, anext, part * AJ / NPART, (part + 1) * AJ / NPART);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      bf16x8_t af[FM], bfr[FN];
-      const int chunk = (kk >> 3) + (lane >> 5);
+    for (int j = 0; j < FJ; ++j) af[0][j] = *(const bf16x8_t*)(Ab + j * 32 * A_ROW + a_rd[0]);
 #pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        const int row = wm * FM * 32 + i * 32 + (lane & 31);
-        af[i] = *(const bf16x8_t*)(Ab + row * (BK * 2) + lds_slot(row, chunk) * 16);
-      }
+    for (int s2 = 0; s2 < 4; s2 += 2) {
+      __builtin_amdgcn_sched_barrier(0);
+      issue_a(sb3, std::integral_constant<int, SUB3>{}, anext, (s2 / 2) * AJ / 2, (s2 / 2 + 1) * AJ / 2);
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        int brow;
-        if constexpr (GATEUP) {
-          brow = (j < FN / 2) ? (wn * (FN / 2) * 32 + j * 32) : (BNW / 2 + wn * (FN / 2) * 32 + (j - FN / 2) * 32);
-        } else {
-          brow = wn * FN * 32 + j * 32;
+      for (int j = 0; j < FJ; ++j) af[1][j] = *(const bf16x8_t*)(Ab + j * 32 * A_ROW + a_rd[s2 + 1]);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int s = s2 + t;
+        bf16x8_t wf[FI];
+#pragma unroll
+        for (int i = 0; i < FI; ++i) {
+          u32x4_t v = {wv[cur][i][4 * s], wv[cur][i][4 * s + 1], wv[cur][i][4 * s + 2], wv[cur][i][4 * s + 3]};
+          wf[i] = __builtin_bit_cast(bf16x8_t, v);
         }
-        const int row = brow + (lane & 31);
-        bfr[j] = *(const bf16x8_t*)(Bb + row * (BK * 2) + lds_slot(row, chunk) * 16);
-      }
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
+        for (int j = 0; j < FJ; ++j)
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
-      // the decode of the next step, spread over the MFMA sub-steps
-      if ((kk / 16) % (4 / PIECES) == 0) {
-        const int p = (kk / 16) / (4 / PIECES);
-        BP::template decode<SUB1>(raw[buf ^ 1][p], grid_lds, breg);
-        store_b(breg, p, buf ^ 1);
+          for (int i = 0; i < FI; ++i)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[i], af[t][j], acc[i][j], 0, 0, 0);
+        if (t == 0 && s2 == 0) {
+#pragma unroll
+          for (int j = 0; j < FJ; ++j) af[0][j] = *(const bf16x8_t*)(Ab + j * 32 * A_ROW + a_rd[2]);
+        }
       }
+      BP::template decode<SUB1>(SUB == 3 ? head_nxt[s2 / 2] : head[s2 / 2], raw[cur ^ 1][s2 / 2], grid_lds,
+                                wv[cur ^ 1][s2 / 2]);
+      // schedule: the loads first, then 32 x (1 MFMA, 4 VALU), an LDS read after every
+      // other MFMA
+      __builtin_amdgcn_sched_group_barrier(0x020, AJ / 2, 0);
+#pragma unroll
+      for (int m = 0; m < NMR; ++m) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 128 / NMR, 0);
+        if (m % DSR == 0) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    // A(k+1) has landed once at most the newest AJ VMEM ops (the A loads of step k+2) are
-    // outstanding (vmcnt field in bits 3:0 and 15:14; expcnt 7 and lgkmcnt 15 = no wait);
-    // with AD == 2 everything must land
-    if constexpr (AD == 3) {
-      static_assert(AJ < 16, "vmcnt encoding");
-      __builtin_amdgcn_s_waitcnt(AJ | (7 << 4) | (15 << 8));
-    } else {
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this thread's B stores
+    // A(k+1) has landed once at most the newest AJ VMEM ops (the loads of A(k+3)) are
+    // outstanding
+    static_assert(AJ < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt(wait_vmcnt(AJ));
     lds_barrier();
     abuf = abuf + 1 == AD ? 0 : abuf + 1;
+    if constexpr (SUB == 3) {
+#pragma unroll
+      for (int i = 0; i < FI; ++i) head[i] = head_nxt[i];
+    }
   };
   for (int sb = 0; sb < nsb; ++sb) {
     step(sb, S0{});
@@ -420,50 +425,60 @@ __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restr
     step(sb, S2{});
     step(sb, S3{});
   }
-
   __builtin_amdgcn_s_waitcnt(0);  // the clamped prefetches of the last steps
-  __syncthreads();
+  __syncthreads();                 // every wave is done with the activation buffers
 
-  // ---- epilogue through LDS. 32x32 accumulator layout: lane l, element r -> column l%32,
-  // row 8*(r/4) + 4*(l/32) + r%4. The C tile is staged as bf16 in LDS, then written out
-  // in 16-byte row chunks.
-  uint16_t* cs = (uint16_t*)smem;
-  const int col = lane & 31;
+  // ---- epilogue: the bf16 C tile is staged in LDS (rows of CW 16-byte chunks, chunk c of
+  // row r at slot c ^ (r % CW)), then written out as whole rows, 16 bytes per lane.
+  // Accumulator layout: lane l holds route 32 j + l % 32 and weight rows
+  // 8 (r / 4) + 4 (l / 32) + r % 4 of fragment i: 4 consecutive columns per (i, j, r / 4).
+  constexpr int CCOLS = GATEUP ? BNW / 2 : BNW;  // output columns of the tile
+  constexpr int CW = CCOLS / 8;                  // 16-byte chunks per row
+  static_assert(BM * CCOLS * 2 <= AD * A_BYTES, "C tile fits the activation buffers");
+  uint8_t* cs = smem;
+  auto c_put = [&](int row, int col, uint32_t lo, uint32_t hi) {
+    const int c = col >> 3;
+    u32x2_t v = {lo, hi};
+    *(u32x2_t*)(cs + row * (CW * 16) + 16 * (c ^ (row % CW)) + 2 * (col & 7)) = v;
+  };
   if constexpr (GATEUP) {
+    constexpr int FH = FI / 2;
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int j = 0; j < FJ; ++j) {
+      const int ml = 32 * (wm * FJ + j) + l32;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int ml = wm * FM * 32 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      for (int i = 0; i < FH; ++i)
 #pragma unroll
-        for (int j = 0; j < FN / 2; ++j)
-          cs[ml * CPITCH_UP + wn * (FN / 2) * 32 + j * 32 + col] = f2bf(silu_mul(acc[i][j][r], acc[i][j + FN / 2][r]));
-      }
-    __syncthreads();
-    constexpr int CW = BNW / 2 / 8;  // 16-byte chunks per row
-    const int n0 = nt * (BNW / 2);
-    for (int c = tid; c < BM * CW; c += NTHREADS) {
-      const int ml = c / CW, q = c % CW;
-      if (ml < valid)
-        *(u32x4_t*)(out + (int64_t)(m0 + ml) * NI + n0 + 8 * q) = *(const u32x4_t*)(cs + ml * CPITCH_UP + 8 * q);
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const f32x16_t& g = acc[i][j];
+          const f32x16_t& u = acc[i + FH][j];
+          c_put(ml, (wn * FH + i) * 32 + 8 * r4 + 4 * h,
+                f2bf2(silu_mul(g[4 * r4], u[4 * r4]), silu_mul(g[4 * r4 + 1], u[4 * r4 + 1])),
+                f2bf2(silu_mul(g[4 * r4 + 2], u[4 * r4 + 2]), silu_mul(g[4 * r4 + 3], u[4 * r4 + 3])));
+        }
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int j = 0; j < FJ; ++j) {
+      const int ml = 32 * (wm * FJ + j) + l32;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int ml = wm * FM * 32 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      for (int i = 0; i < FI; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) cs[ml * CPITCH_DN + wn * FN * 32 + j * 32 + col] = f2bf(acc[i][j][r]);
-      }
-    __syncthreads();
-    constexpr int CW = BNW / 8;
-    for (int c = tid; c < BM * CW; c += NTHREADS) {
-      const int ml = c / CW, q = c % CW;
-      if (ml < valid) {
-        const int64_t p = perm[m0 + ml];
-        *(u32x4_t*)(out + p * NI + (int64_t)nt * BNW + 8 * q) = *(const u32x4_t*)(cs + ml * CPITCH_DN + 8 * q);
-      }
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const f32x16_t& a = acc[i][j];
+          c_put(ml, (wn * FI + i) * 32 + 8 * r4 + 4 * h, f2bf2(a[4 * r4], a[4 * r4 + 1]),
+                f2bf2(a[4 * r4 + 2], a[4 * r4 + 3]));
+        }
+    }
+  }
+  __syncthreads();
+  const int64_t col0 = (int64_t)nt * CCOLS;
+  for (int q = tid; q < BM * CW; q += NTHREADS) {
+    const int ml = q / CW, c = q % CW;
+    if (ml < valid) {
+      const u32x4_t v = *(const u32x4_t*)(cs + ml * (CW * 16) + 16 * (c ^ (ml % CW)));
+      const int64_t orow = GATEUP ? (int64_t)(m0 + ml) : (int64_t)perm[m0 + ml];
+      *(u32x4_t*)(out + orow * NI + col0 + 8 * c) = v;
     }
   }
 }
@@ -498,22 +513,23 @@ __global__ __launch_bounds__(256) void combine_routes(const uint16_t* __restrict
 }
 
 template <int TYPE, bool GATEUP>
-void launch_gemm(dim3 grid, hipStream_t stream, const uint16_t* A_src, const int32_t* perm, const int32_t* seg,
-                 const int32_t* tseg, int S, int top_k, const void* W, int w_is_table, int64_t w_expert_stride,
+void launch_gemm(dim3 grid, hipStream_t stream, const uint16_t* A_src, uint32_t a_bytes, const int32_t* perm, const int32_t* seg,
+                 const int32_t* tseg, const int32_t* tile_slot, int S, int top_k, const void* W, int w_is_table, int64_t w_expert_stride,
                  int64_t rb, int Kdim, int NI, int NT, int64_t nblk, uint16_t* out) {
-  grouped_gemm<TYPE, GATEUP><<<grid, NTHREADS, 0, stream>>>(A_src, perm, seg, tseg, S, top_k, (const uint8_t*)W,
+  grouped_gemm<TYPE, GATEUP><<<grid, NTHREADS, 0, stream>>>(A_src, a_bytes, perm, seg, tseg, tile_slot, S, top_k, (const uint8_t*)W,
                                                              w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out);
 }
 
 template <bool GATEUP>
-int dispatch_gemm(int type, dim3 grid, hipStream_t stream, const uint16_t* A_src, const int32_t* perm,
-                  const int32_t* seg, const int32_t* tseg, int S, int top_k, const void* W, int w_is_table,
+int dispatch_gemm(int type, dim3 grid, hipStream_t stream, const uint16_t* A_src, uint32_t a_bytes,
+                  const int32_t* perm,
+                  const int32_t* seg, const int32_t* tseg, const int32_t* tile_slot, int S, int top_k, const void* W, int w_is_table,
                   int64_t w_expert_stride, int64_t rb, int Kdim, int NI, int NT, int64_t nblk, uint16_t* out) {
   switch (type) {
-    case GGML_Q8_0: launch_gemm<GGML_Q8_0, GATEUP>(grid, stream, A_src, perm, seg, tseg, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
-    case GGML_Q4_K: launch_gemm<GGML_Q4_K, GATEUP>(grid, stream, A_src, perm, seg, tseg, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
-    case GGML_Q6_K: launch_gemm<GGML_Q6_K, GATEUP>(grid, stream, A_src, perm, seg, tseg, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
-    case GGML_IQ3_S: launch_gemm<GGML_IQ3_S, GATEUP>(grid, stream, A_src, perm, seg, tseg, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
+    case GGML_Q8_0: launch_gemm<GGML_Q8_0, GATEUP>(grid, stream, A_src, a_bytes, perm, seg, tseg, tile_slot, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
+    case GGML_Q4_K: launch_gemm<GGML_Q4_K, GATEUP>(grid, stream, A_src, a_bytes, perm, seg, tseg, tile_slot, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
+    case GGML_Q6_K: launch_gemm<GGML_Q6_K, GATEUP>(grid, stream, A_src, a_bytes, perm, seg, tseg, tile_slot, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
+    case GGML_IQ3_S: launch_gemm<GGML_IQ3_S, GATEUP>(grid, stream, A_src, a_bytes, perm, seg, tseg, tile_slot, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
     default: set_error("grouped GEMM: ggml type %d has no kernel", type); return KTMI_ETYPE;
   }
   KTMI_HIP_TRY(hipGetLastError());
@@ -534,6 +550,7 @@ GroupedPlan grouped_plan(int64_t tokens, int64_t top_k, int64_t n_slots, int64_t
   P.off_counts = o; o = align256(o + ((nch > 0 ? nch : 1) * n_slots + n_slots) * 4);
   P.off_seg = o; o = align256(o + (n_slots + 1) * 4);
   P.off_tseg = o; o = align256(o + (n_slots + 1) * 4);
+  P.off_tslot = o; o = align256(o + P.max_tiles * 4);
   P.off_perm = o; o = align256(o + P.routes * 4);
   P.off_h = o; o = align256(o + P.routes * inter * 2);
   P.off_y = o; o = align256(o + P.routes * hidden * 2);
@@ -552,11 +569,14 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
                (long long)K, BNW > 256 ? BNW : 256);
   KTMI_REQUIRE(N % (BNW / 2) == 0 && N % 256 == 0, KTMI_EINVAL,
                "grouped layer: intermediate %lld not a multiple of 256", (long long)N);
+  KTMI_REQUIRE(tokens * K * 2 <= 0xFFFFFFFFll && R * N * 2 <= 0xFFFFFFFFll, KTMI_EINVAL,
+               "grouped layer: activations of %lld tokens exceed the 4 GiB buffer range", (long long)tokens);
   if (tokens == 0) return KTMI_OK;
   int32_t* hist = (int32_t*)(ws + P.off_counts);
   int32_t* seg = (int32_t*)(ws + P.off_seg);
   int32_t* tseg = (int32_t*)(ws + P.off_tseg);
   int32_t* perm = (int32_t*)(ws + P.off_perm);
+  int32_t* tile_slot = (int32_t*)(ws + P.off_tslot);
   uint16_t* H = (uint16_t*)(ws + P.off_h);
   uint16_t* Y = (uint16_t*)(ws + P.off_y);
   const int64_t nch = (R + CHW - 1) / CHW;
@@ -565,7 +585,7 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
   record_stage(0, stream);
   sort_count<<<sblocks, SORT_THREADS, 0, stream>>>(slot_ids, R, S, hist, nch);
   sort_scan_chunks<<<S, SORT_THREADS, 0, stream>>>(hist, nch, tot);
-  sort_scan_slots<<<1, SORT_THREADS, 0, stream>>>(tot, S, seg, tseg, BM);
+  sort_scan_slots<<<1, SORT_THREADS, 0, stream>>>(tot, S, seg, tseg, tile_slot, BM);
   sort_scatter<<<sblocks, SORT_THREADS, 0, stream>>>(slot_ids, R, S, hist, nch, seg, perm);
   KTMI_HIP_TRY(hipGetLastError());
   record_stage(1, stream);
@@ -574,7 +594,7 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
   const int NT1 = (int)(N / (BNW / 2));
   const int64_t nblk1 = P.max_tiles * NT1;
   dim3 g1((unsigned)((nblk1 + 8 * NT1 - 1) / (8 * NT1) * (8 * NT1)));
-  int rc = dispatch_gemm<true>(L->type13, g1, stream, x, perm, seg, tseg, S, (int)top_k, L->w13, L->w_is_table,
+  int rc = dispatch_gemm<true>(L->type13, g1, stream, x, (uint32_t)(tokens * K * 2), perm, seg, tseg, tile_slot, S, (int)top_k, L->w13, L->w_is_table,
                                st13, rb13, (int)K, (int)N, NT1, nblk1, H);
   if (rc) return rc;
   record_stage(2, stream);  // no mid stage on this path: SiLU*mul is in the gate/up epilogue
@@ -582,7 +602,7 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
   const int NT2 = (int)(K / BNW);
   const int64_t nblk2 = P.max_tiles * NT2;
   dim3 g2((unsigned)((nblk2 + 8 * NT2 - 1) / (8 * NT2) * (8 * NT2)));
-  rc = dispatch_gemm<false>(L->type2, g2, stream, H, perm, seg, tseg, S, (int)top_k, L->w2, L->w_is_table, st2, rb2,
+  rc = dispatch_gemm<false>(L->type2, g2, stream, H, (uint32_t)(R * N * 2), perm, seg, tseg, tile_slot, S, (int)top_k, L->w2, L->w_is_table, st2, rb2,
                             (int)N, (int)K, NT2, nblk2, Y);
   if (rc) return rc;
   record_stage(4, stream);
