@@ -15,8 +15,9 @@ nothing. KT_HOT_LAYER_MODE=auto|gemv|grouped overrides the choice.
 
 Weights come from an expert source: an object with E, inter, K, types(layer_idx) and
 slice(layer_idx, proj, N, rank, experts) -> uint8 [n, rows, part_row_bytes] (the
-reference's _GGUFExperts, :109-160). `register_source(path, source)` binds one to the
-kt_config.weight_path the method is built with.
+reference's _GGUFExperts, :109-160). `GGUFExperts` is that source over a GGUF file (one
+reader per path, shared by all layers); `register_source(path, source)` binds any other
+source to the kt_config.weight_path the method is built with.
 """
 from __future__ import annotations
 
@@ -27,8 +28,9 @@ from typing import Dict
 
 import torch
 
+
 from . import _lib
-from .gguf import BLOCK_INFO, KERNEL_TYPES, row_bytes as _row_bytes
+from .gguf import BLOCK_INFO, KERNEL_TYPES, GGUFFile, row_bytes as _row_bytes
 
 try:  # inside SGLang the real combine input type is used
     from sglang.srt.layers.moe.token_dispatcher import StandardCombineInput  # type: ignore
@@ -46,18 +48,83 @@ def _log(msg):
     print(f"[kt-gguf-hot {time.strftime('%H:%M:%S')}] {msg}", flush=True)
 
 
+class GGUFExperts:
+    """The routed experts of a GGUF file (hot/kt_gguf_hot.py:109-160): per layer the
+    tensors blk.{l}.ffn_{gate,up,down}_exps.weight, shapes [E, inter, K] (gate, up) and
+    [E, K, inter] (down), read as views over the file mapping."""
+
+    def __init__(self, path: str):
+        self.file = GGUFFile(path)
+        cfg = self.file.model_config()
+        self.E = cfg["num_experts"]
+        self.inter = cfg["moe_intermediate_size"]
+        self.K = cfg["hidden_size"]
+        self.num_layers = cfg["num_layers"]
+
+    def _raw(self, name: str):
+        """(uint8 torch view of the tensor's bytes over the mapping, ggml type)."""
+        import warnings
+
+        data = self.file.raw(name)
+        with warnings.catch_warnings():
+            warnings.simplefilter("ignore")  # read-only buffer, only copied out
+            return torch.from_numpy(data), self.file.ggml_type(name)
+
+    def types(self, layer_idx: int):
+        return tuple(self.file.ggml_type(f"blk.{layer_idx}.ffn_{p}_exps.weight") for p in ("gate", "up", "down"))
+
+    def _view(self, layer_idx: int, proj: str, N: int, rank: int) -> torch.Tensor:
+        """This rank's TP part of every expert: rows [N*rank, N*(rank+1)) of gate/up, the
+        matching block-aligned columns of down; uint8 [E, rows, part_row_bytes]."""
+        data, t = self._raw(f"blk.{layer_idx}.ffn_{proj}_exps.weight")
+        blck, ts = BLOCK_INFO[t]
+        if proj != "down":
+            if self.K % blck:
+                raise ValueError(f"layer {layer_idx} {proj}: hidden {self.K} is not whole blocks of {blck}")
+            return data.view(self.E, self.inter, (self.K // blck) * ts)[:, N * rank:N * (rank + 1), :]
+        if self.inter % blck or (N * rank) % blck or N % blck:
+            raise ValueError(f"layer {layer_idx} down: slice [{N * rank}, {N * (rank + 1)}) of {self.inter} is not "
+                             f"block-aligned ({blck})")
+        v = data.view(self.E, self.K, self.inter // blck, ts)[:, :, (N * rank) // blck:(N * (rank + 1)) // blck, :]
+        return v.reshape(self.E, self.K, -1)
+
+    def slice(self, layer_idx: int, proj: str, N: int, rank: int, experts) -> torch.Tensor:
+        """Raw bytes of this rank's part of the given logical experts: uint8
+        [len(experts), rows, part_row_bytes] (a copy)."""
+        ids = torch.as_tensor(experts, dtype=torch.int64)
+        return self._view(layer_idx, proj, N, rank)[ids].contiguous()
+
+    def banks(self, layer_idx: int, N: int, rank: int = 0, p2l=None, pin: bool = True):
+        """[gate, up, down]: this rank's part of every expert of the layer as uint8
+        [E, part_bytes] in host memory (pinned when a GPU is present), physical order
+        p2l[physical] = logical when a placement map is given (P:40712-40752)."""
+        out = []
+        pin = pin and torch.cuda.is_available()
+        for proj in ("gate", "up", "down"):
+            v = self._view(layer_idx, proj, N, rank).reshape(self.E, -1)
+            if p2l is not None:
+                v = v[torch.as_tensor(p2l, dtype=torch.int64)]
+            h = torch.empty(v.shape, dtype=torch.uint8, pin_memory=pin)
+            h.copy_(v)
+            out.append(h)
+        return out
+
+
 _sources: Dict[str, object] = {}
 
 
 def register_source(path: str, source) -> None:
-    """Bind an expert source to a weight path (what the reference opens as a GGUF)."""
+    """Bind an expert source to a weight path (instead of opening it as a GGUF file)."""
     _sources[path] = source
 
 
 def _reader(path: str):
+    """The registered source for the path, else the (cached) GGUF reader of the file."""
     src = _sources.get(path)
     if src is None:
-        raise RuntimeError(f"no expert source registered for {path!r} (register_source)")
+        if not path or not os.path.isfile(path):
+            raise RuntimeError(f"no expert source registered for {path!r} and no GGUF file there")
+        src = _sources[path] = GGUFExperts(path)
     return src
 
 

@@ -12,6 +12,12 @@ KT_HOT_INTERVAL decode steps (:376-432): counts read one round late through a pi
 buffer, decayed by KT_HOT_DECAY; per layer the coldest residents give way to the hottest
 non-residents when candidate > KT_HOT_MARGIN * resident, at most KT_HOT_SWAPS per layer;
 a swap copies the expert's bytes from the pinned bank into the slot (`fill`, :245-271).
+The banks are the streamer's when one is loaded (one pinned copy serves both), else the
+cache's own, built from the hot method's expert reader (`_bank`, :157-214;
+KT_HOT_BANKS=own forces these).
+
+Out of scope here: the KV-lending slots (lend_slot / take_back_slot, the base tables) and
+the Q2_0 -> Q8_0 down repack.
 """
 from __future__ import annotations
 
@@ -30,6 +36,8 @@ MAX_SWAPS = int(os.environ.get("KT_HOT_SWAPS", "8"))
 DECAY = float(os.environ.get("KT_HOT_DECAY", "0.9"))
 MARGIN = float(os.environ.get("KT_HOT_MARGIN", "1.5"))
 SEED = os.environ.get("KT_HOT_SEED")
+OWN_BANKS = os.environ.get("KT_HOT_BANKS", "")
+LOG_EVERY = int(os.environ.get("KT_HOT_LOG_EVERY", "0") or 0)
 EMPTY, ABSENT = -1, -2
 
 
@@ -62,7 +70,7 @@ class HotCache:
         self.S = slots
         self.slot2log: List[List[int]] = [[EMPTY] * slots for _ in range(num_layers)]
         self.layers: Dict[int, tuple] = {}  # layer_idx -> (hot method, layer)
-        self.banks: Dict[int, list] = {}    # layer_idx -> [gate, up, down] pinned uint8 [E, part_bytes]
+        self.banks: Dict[int, list] = {}    # own banks: layer_idx -> [gate, up, down] pinned uint8 [E, part]
         pin = self.device.type == "cuda"
         self._counts_host = torch.zeros((num_layers, num_experts), dtype=torch.float32, pin_memory=pin)
         self._counts_event = None
@@ -95,10 +103,32 @@ class HotCache:
             self.log2slot_cpu[layer_idx, logical] = slot
             self.log2cpu_cpu[layer_idx, logical] = -1
 
+    def _bank(self, layer_idx: int):
+        """[gate, up, down] uint8 [E, part bytes] in pinned host memory, physical order:
+        the streamer's bank when it is loaded, else the cache's own from the hot method's
+        reader (hot/kt_hot_cache.py:157-214)."""
+        b = self.banks.get(layer_idx)
+        if b is not None:
+            return b
+        if OWN_BANKS != "own":
+            from . import kt_stream_prefill as SP
+
+            inst = SP._instance
+            if inst is not None and (inst.reader is not None or layer_idx in inst._banks):
+                return inst._bank(layer_idx)
+        t0 = time.time()
+        method, _layer = self.layers[layer_idx]
+        b = method.reader.banks(layer_idx, method.N, getattr(method, "rank", 0), None)
+        self.banks[layer_idx] = b
+        if layer_idx == min(self.layers):
+            _log(f"rank {self.rank}: layer {layer_idx} own bank {sum(t.numel() for t in b) / 1e9:.2f} GB pinned in "
+                 f"{time.time() - t0:.1f} s (no streamer)")
+        return b
+
     def fill(self, layer_idx: int, slot: int, logical: int) -> None:
         """Copy an expert's bytes from the layer's pinned bank into a slot (async H2D)."""
         method, layer = self.layers[layer_idx]
-        gate, up, down = self.banks[layer_idx]
+        gate, up, down = self._bank(layer_idx)
         N = method.N
         w13, w2 = layer.w13_qweight.data, layer.w2_qweight.data
         g = gate[logical].view(N, -1)
@@ -129,19 +159,48 @@ class HotCache:
                     return f"layer {li} slot {sl} holds {e} but the table says {int(s_cpu[li, e])}"
         return ""
 
+    def fill_empty(self, counts: torch.Tensor, seed_rank: Optional[torch.Tensor] = None) -> int:
+        """Fill every EMPTY slot with the hottest non-residents of its layer (counts [L, E]
+        on the host; ties broken by the seed map's order, seed_rank[l, e] = rank of e).
+        Host tables only; the caller pushes them (hot/kt_hot_cache.py:334-353)."""
+        n = 0
+        for li in sorted(self.layers) if self.layers else range(self.L):
+            empty = [s_ for s_, e in enumerate(self.slot2log[li]) if e == EMPTY]
+            if not empty:
+                continue
+            score = counts[li].double().clone()
+            if seed_rank is not None:
+                score = score + (self.E - seed_rank[li].double()) / (self.E + 1) * 1e-3
+            res = [e for e in self.slot2log[li] if e >= 0]
+            if res:
+                score[torch.tensor(res)] = float("-inf")
+            for s_, c in zip(empty, torch.topk(score, len(empty)).indices.tolist()):
+                self._set(li, s_, c)
+                if li in self.layers:
+                    self.fill(li, s_, c)
+                n += 1
+        return n
+
     def seed(self, placement: Optional[str] = None, p2l=None) -> None:
         """Initial residents: the placement map's first N per layer (filled from the banks)
         or logical 0..N-1 (what the loader put in the slots)."""
+        t0 = time.time()
         if placement:
             p2l = json.load(open(placement))["physical_to_logical_map"]
         for li in sorted(self.layers) if self.layers else range(self.L):
             for s in range(self.N):
                 e = int(p2l[li][s]) if p2l is not None else s
                 self._set(li, s, e)
-                if p2l is not None and e != s and li in self.banks:
+                if p2l is not None and e != s and li in self.layers:
                     self.fill(li, s, e)
         self.push_tables()
         self.ready = True
+        if self.layers:
+            _log(f"rank {self.rank}: {len(self.layers)} layers x {self.N} slots seeded from "
+                 f"{placement or ('a placement map' if p2l is not None else 'logical order')} in {time.time() - t0:.1f} s "
+                 f"({self.bytes / 1e9:.2f} GB copied); interval {INTERVAL}, max {MAX_SWAPS} swaps/layer, "
+                 f"decay {DECAY}, margin {MARGIN}")
+        self.bytes = 0
 
     # -- policy, between steps --------------------------------------------------------
 
@@ -162,7 +221,15 @@ class HotCache:
         do = ((cand_score > 0) & (cand_score > MARGIN * rs)).to(torch.int64).cumprod(1).bool()
         return [(li, int(order[li, j]), int(cand_idx[li, j])) for li, j in do.nonzero().tolist()]
 
-    def before_forward(self, is_decode: bool = True) -> None:
+    def before_forward(self, forward_batch=True) -> None:
+        """Between steps: the swap policy every INTERVAL decode steps (and, under MTP, the
+        target's verify steps). forward_batch: SGLang's ForwardBatch (its forward_mode), or a
+        bool meaning "this is a decode step"."""
+        mode = getattr(forward_batch, "forward_mode", None)
+        if mode is not None:
+            is_decode = mode.is_decode() or (hasattr(mode, "is_target_verify") and mode.is_target_verify())
+        else:
+            is_decode = bool(forward_batch)
         if not self.ready or not is_decode:
             return
         self.step += 1
@@ -184,38 +251,54 @@ class HotCache:
             if li not in self.layers:
                 continue
             self._set(li, s_, c)
-            if li in self.banks:
-                self.fill(li, s_, c)
+            self.fill(li, s_, c)
             swaps += 1
         if swaps:
             self.push_tables()
         self.rounds += 1
         self.swaps += swaps
         self.swap_s += time.time() - t0
+        if self.rounds == 1 or (LOG_EVERY and self.rounds % LOG_EVERY == 0) or self.rounds % 64 == 0:
+            _log(f"rank {self.rank}: round {self.rounds} (step {self.step}): {swaps} swaps this round, "
+                 f"{self.swaps} total, {self.bytes / 1e9:.2f} GB, {self.swap_s * 1e3 / self.rounds:.1f} ms/round; "
+                 f"GPU share of recent routes {self.gpu_share(counts):.3f}")
+
+    def gpu_share(self, counts: torch.Tensor) -> float:
+        """Fraction of the counted routes whose expert is resident now (host counts [L, E])."""
+        res = torch.tensor(self.slot2log)
+        hit = counts.gather(1, res.clamp(min=0)) * (res >= 0)
+        return float(hit.sum()) / max(float(counts.sum()), 1.0)
 
 
 _cache: Optional[HotCache] = None
 
 
-def register(method, layer, num_layers: int, num_experts: int) -> Optional[HotCache]:
-    """Called per layer; the cache is built on the first call and seeded once every layer
-    is known (hot/kt_hot_cache.py:438-455)."""
+def register(method, layer, num_layers: Optional[int] = None, num_experts: Optional[int] = None) -> Optional[HotCache]:
+    """Called by the KT wrapper on its first decode apply of each layer; the cache is built
+    on the first call and seeded once every layer is known (hot/kt_hot_cache.py:438-455).
+    method: the KT wrapper method (kt_config, global_num_experts, tp_rank, gpu_method) or
+    the hot GPU method itself with num_layers / num_experts given."""
     global _cache
     if not ENABLED:
         return None
     kt = method.kt_config
+    gpu = getattr(method, "gpu_method", method)
+    L = getattr(kt, "num_layers", None) or num_layers
+    E = getattr(method, "global_num_experts", None) or num_experts
+    if L is None or E is None:
+        raise RuntimeError("hot cache register: the number of layers and experts is unknown")
     if _cache is None:
         if kt.num_gpu_experts <= 0:
             raise RuntimeError("KT_HOT_DYNAMIC=1 needs num_gpu_experts > 0")
-        _cache = HotCache(num_layers, num_experts, kt.num_gpu_experts, layer.w13_qweight.device)
+        _cache = HotCache(L, E, kt.num_gpu_experts, layer.w13_qweight.device, getattr(method, "tp_rank", 0))
     c = _cache
     if kt.layer_idx not in c.layers:
-        c.layers[kt.layer_idx] = (method, layer)
-        if len(c.layers) == num_layers:
+        c.layers[kt.layer_idx] = (gpu, layer)
+        if len(c.layers) == L:
             c.seed(SEED)
     return c if c.ready else None
 
 
-def before_forward(is_decode: bool = True) -> None:
+def before_forward(forward_batch=True) -> None:
     if _cache is not None:
-        _cache.before_forward(is_decode)
+        _cache.before_forward(forward_batch)

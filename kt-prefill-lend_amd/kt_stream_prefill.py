@@ -13,8 +13,9 @@ Differences from the reference, on purpose:
   * the slots hold the raw blocks in the layout the grouped kernels read, so there is no
     bf16 copy of each group's weights (the reference dequantises into w13_bf16 / w2_bf16,
     P:40789-40798) and no CUTLASS workspace;
-  * banks are handed in as pinned tensors (`set_bank`); reading them from the GGUF file is
-    the loader's job;
+  * banks are built lazily per layer from an expert reader (`reader=`: a GGUFExperts over
+    the GGUF file, or any source with banks(layer, N, rank, p2l)), as the reference's
+    _bank does (P:40712-40752), or handed in as pinned tensors (`set_bank`);
   * `run` takes plain tensors (x, topk weights, expert ids); `run_layers` pipelines whole
     layers, so layer l+1's weights stream in while layer l computes.
 
@@ -100,8 +101,10 @@ class KTStreamPrefillGGUF:
     """Process-wide (per device) streaming state shared by every MoE layer (P:40641)."""
 
     def __init__(self, N: int, K: int, top_k: int, types: Tuple[int, int, int], group_size: int = GROUP_SIZE,
-                 device=None, n_slots: int = 2):
+                 device=None, n_slots: int = 2, reader=None, rank: int = 0, p2l=None):
         self.N, self.K, self.top_k, self.G = N, K, top_k, group_size
+        self.reader, self.rank = reader, rank
+        self._p2l = p2l  # layer -> physical_to_logical list, or None
         self.device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
         self.types = tuple(types)
         pg, pu, pd = part_bytes(self.types, N, K)
@@ -142,10 +145,31 @@ class KTStreamPrefillGGUF:
         self._banks[layer_idx] = bank
 
     def bank(self, layer_idx: int) -> Bank:
+        """The layer's bank: set_bank's, or built on first use from the reader (this rank's
+        part of every expert, physical order under a placement map)."""
         b = self._banks.get(layer_idx)
         if b is None:
-            raise RuntimeError(f"no bank for layer {layer_idx} (set_bank)")
+            if self.reader is None:
+                raise RuntimeError(f"no bank for layer {layer_idx} (set_bank, or a reader)")
+            t0 = time.time()
+            types = tuple(self.reader.types(layer_idx))
+            p2l = self._p2l.get(layer_idx) if isinstance(self._p2l, dict) else None
+            gate, up, down = self.reader.banks(layer_idx, self.N, self.rank, p2l)
+            b = Bank(gate, up, down, types)
+            self.set_bank(layer_idx, b)
+            if TIMING or len(self._banks) == 1:
+                _log(f"rank {self.rank}: layer {layer_idx} bank {sum(t.numel() for t in (gate, up, down)) / 1e9:.2f} GB "
+                     f"pinned in {time.time() - t0:.1f} s (types {types}{', placement map' if p2l is not None else ''})")
         return b
+
+    def _bank(self, layer_idx: int):
+        """[gate, up, down] of the layer's bank (the hot cache fills its slots from these)."""
+        b = self.bank(layer_idx)
+        return [b.gate, b.up, b.down]
+
+    def build_all_banks(self, layers: Sequence[int]):
+        for li in layers:
+            self.bank(li)
 
     # -- staging and one group --------------------------------------------------
 
@@ -252,14 +276,14 @@ class KTStreamPrefillGGUF:
 _instance: Optional[KTStreamPrefillGGUF] = None
 
 
-def preallocate(N: int, K: int, top_k: int, types, device=None) -> Optional[KTStreamPrefillGGUF]:
+def preallocate(N: int, K: int, top_k: int, types, device=None, reader=None, rank: int = 0) -> Optional[KTStreamPrefillGGUF]:
     """Create the process-wide streamer early (its slots count toward the memory budget
     before the KV pool is sized, P:40607-40636); a no-op when streaming is off."""
     global _instance
     if STREAM_THRESHOLD <= 0:
         return None
     if _instance is None:
-        _instance = KTStreamPrefillGGUF(N, K, top_k, types, GROUP_SIZE, device)
+        _instance = KTStreamPrefillGGUF(N, K, top_k, types, GROUP_SIZE, device, reader=reader, rank=rank)
     return _instance
 
 

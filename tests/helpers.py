@@ -40,3 +40,27 @@ def gemv_layer_oracle(x_bits, topk_w, slot_ids, w13, w2, types, hidden, inter):
     h = R.silu_and_mul(h13)
     out = R.bf16_bits(R.moe_a8_vec(R.bf16_to_f32(h), w2, ids, 1, types[2], hidden, T * k).astype(np.float32))
     return R.combine(out.reshape(T, k, hidden), topk_w)
+
+
+def make_expert_gguf(path, layers: int, E: int, N: int, K: int, types, seed: int = 7, metadata: bool = True,
+                     world: int = 1):
+    """A GGUF file with the routed-expert tensors of `layers` layers: blk.{l}.ffn_{gate,up,
+    down}_exps.weight, shapes [E, N*world, K] and [E, K, N*world], random weights ~N(0, 0.02)
+    quantised to `types` (gate, up, down). Returns {(layer, proj): uint8 [E, rows, rb]}."""
+    from kt_prefill_lend_amd import gguf as G
+
+    rng = np.random.default_rng(seed)
+    I = N * world
+    raw, tensors = {}, []
+    for li in range(layers):
+        for proj, t, (rows, cols) in (("gate", types[0], (I, K)), ("up", types[1], (I, K)), ("down", types[2], (K, I))):
+            w = (rng.standard_normal((E * rows, cols), dtype=np.float32) * np.float32(0.02))
+            q = G.quantize_rows(w, t).reshape(E, rows, -1)
+            raw[(li, proj)] = q
+            tensors.append((f"blk.{li}.ffn_{proj}_exps.weight", (E, rows, cols), t, q))
+    md = {"general.architecture": "toymoe", "general.name": "synthetic experts"}
+    if metadata:
+        md.update({"toymoe.block_count": layers, "toymoe.expert_count": E, "toymoe.expert_feed_forward_length": I,
+                   "toymoe.embedding_length": K})
+    G.write_gguf(str(path), md, tensors)
+    return raw
