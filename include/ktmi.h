@@ -196,6 +196,38 @@ int ktmi_add_bf16(void* acc, const void* x, int64_t n, void* stream);
 void* ktmi_host_alloc(int64_t bytes);
 int ktmi_host_free(void* p);
 
+/* ---- CPU cold experts and the GPU <-> CPU handoff.
+ * The engine computes a layer's routes to CPU experts on the host cores with the numerics of
+ * kt-kernel's LLAMAFILE MoE forward_many (K:2571-2800): x quantised to Q8_K (Q8_0 for Q8_0
+ * weights), int8 block dot products, silu(gate)*up in fp32 re-quantised for down, fp32
+ * weighted sum in route order, one bf16 rounding. Its weights are a bank of every expert
+ * (ktmi_bank, host memory that outlives the engine); expert ids index the bank, other ids
+ * (-1 for the GPU's residents) add nothing. Types: 8, 12, 14, 21. */
+typedef struct ktmi_cpu_moe ktmi_cpu_moe;
+/* threads <= 0: min(16, host threads). max_tokens x max_top_k sizes the pinned staging
+ * of submit (0 for a forward-only engine). Replaces kt-kernel's MOE construction and
+ * KExpertsCPUBuffer (the wrapper's CPU side). NULL on failure. */
+ktmi_cpu_moe* ktmi_cpu_moe_create(int64_t hidden, int64_t inter, int type13, int type2, const ktmi_bank* bank,
+                                  int threads, int64_t max_tokens, int64_t max_top_k);
+int ktmi_cpu_moe_destroy(ktmi_cpu_moe* h);
+/* Host arrays: x_bf16 [tokens, hidden], expert_ids int32 [tokens, top_k], weights fp32,
+ * out_bf16 [tokens, hidden]; synchronous (forward_many). */
+int ktmi_cpu_moe_forward(ktmi_cpu_moe* h, int64_t tokens, int64_t top_k, const int32_t* expert_ids,
+                         const float* weights, const void* x_bf16, void* out_bf16);
+/* Device arrays on `stream`: staged to pinned host memory after the stream's prior work,
+ * then computed by the engine's worker thread while the stream continues. Replaces
+ * BaseMoEWrapper.submit_forward and kt_uva_handoff.submit (P:10590-10602, P:41240-41270). */
+int ktmi_cpu_moe_submit(ktmi_cpu_moe* h, const void* x_bf16, const int32_t* expert_ids, const float* weights,
+                        int64_t tokens, int64_t top_k, void* stream);
+/* Waits (host) for the submitted layer, then out_bf16 = bf16(out_bf16 + cpu output) on
+ * `stream` (16-byte aligned). Replaces sync_forward + `output + cpu_output` and
+ * kt_uva_handoff.sync_add (P:10598-10602, P:41285-41301). */
+int ktmi_cpu_moe_sync_add(ktmi_cpu_moe* h, void* out_bf16, void* stream);
+int ktmi_cpu_moe_threads(const ktmi_cpu_moe* h);
+/* "avx512-vnni" or "scalar": the engine's int8 dot-product kernels (VNNI when the host has
+ * it, unless KTMI_CPU_ISA=scalar was set at creation) */
+const char* ktmi_cpu_moe_isa(const ktmi_cpu_moe* h);
+
 #ifdef __cplusplus
 }
 #endif

@@ -77,6 +77,13 @@ SIGNATURES = {
     "ktmi_add_bf16": (_i32, [_vp, _vp, _i64, _vp]),
     "ktmi_host_alloc": (_vp, [_i64]),
     "ktmi_host_free": (_i32, [_vp]),
+    "ktmi_cpu_moe_create": (_vp, [_i64, _i64, _i32, _i32, C.POINTER(ktmi_bank), _i32, _i64, _i64]),
+    "ktmi_cpu_moe_destroy": (_i32, [_vp]),
+    "ktmi_cpu_moe_forward": (_i32, [_vp, _i64, _i64, _vp, _vp, _vp, _vp]),
+    "ktmi_cpu_moe_submit": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _vp]),
+    "ktmi_cpu_moe_sync_add": (_i32, [_vp, _vp, _vp]),
+    "ktmi_cpu_moe_threads": (_i32, [_vp]),
+    "ktmi_cpu_moe_isa": (C.c_char_p, [_vp]),
 }
 
 _lib = None

@@ -1,0 +1,216 @@
+// The CPU expert engine behind the C ABI, and the GPU <-> CPU handoff of one MoE layer:
+// kt-kernel's submit_forward / sync_forward as KTEPWrapperMethod calls them around the GPU
+// method (P:10590-10602) and kt_uva_handoff.submit / sync_add (P:41025-41301).
+//
+// submit(x, ids, weights) on the compute stream: three device->host copies into the
+// engine's pinned staging buffers and an event; the engine's worker thread waits for the
+// event, runs the cold routes on the host cores (cpu_moe.cpp) into a pinned bf16 output.
+// The stream goes on with the GPU's hot experts meanwhile. sync_add(out): the host waits
+// for the worker, then a host->device copy of the CPU output and out = bf16(out + cpu) on
+// the stream (the wrapper's `output + cpu_output`). The pinned output is written again
+// only after that copy has completed (event out_free), so back-to-back layers cannot
+// overwrite it early. One submit is outstanding at a time per engine.
+#include <condition_variable>
+#include <mutex>
+#include <thread>
+
+#include "cpu_moe.h"
+#include "kernels.h"
+
+struct ktmi_cpu_moe {
+  ktmi_cpu::Engine* eng = nullptr;
+  int device = 0;
+  int64_t K = 0, max_tokens = 0, max_top_k = 0;
+  uint16_t* x_h = nullptr;
+  int32_t* ids_h = nullptr;
+  float* w_h = nullptr;
+  uint16_t* out_h = nullptr;
+  uint16_t* out_d = nullptr;
+  hipEvent_t in_ready = nullptr, out_free = nullptr;
+  bool out_free_pending = false;
+  std::thread worker;
+  std::mutex m;
+  std::condition_variable cv;
+  enum State { IDLE, SUBMITTED, DONE } state = IDLE;
+  int64_t T = 0, k = 0;
+  int rc = 0;
+  bool stop = false;
+};
+
+namespace {
+
+void worker_loop(ktmi_cpu_moe* h) {
+  (void)hipSetDevice(h->device);
+  for (;;) {
+    {
+      std::unique_lock<std::mutex> g(h->m);
+      h->cv.wait(g, [h] { return h->stop || h->state == ktmi_cpu_moe::SUBMITTED; });
+      if (h->stop) return;
+    }
+    int rc = hipEventSynchronize(h->in_ready) == hipSuccess ? 0 : -2;
+    if (rc == 0 && h->out_free_pending) rc = hipEventSynchronize(h->out_free) == hipSuccess ? 0 : -2;
+    if (rc == 0) rc = ktmi_cpu::engine_forward(h->eng, h->T, h->k, h->ids_h, h->w_h, h->x_h, h->out_h);
+    {
+      std::lock_guard<std::mutex> g(h->m);
+      h->rc = rc;
+      h->state = ktmi_cpu_moe::DONE;
+    }
+    h->cv.notify_all();
+  }
+}
+
+void destroy(ktmi_cpu_moe* h) {
+  if (!h) return;
+  if (h->worker.joinable()) {
+    {
+      std::lock_guard<std::mutex> g(h->m);
+      h->stop = true;
+    }
+    h->cv.notify_all();
+    h->worker.join();
+  }
+  if (h->in_ready || h->x_h || h->out_d) (void)hipSetDevice(h->device);
+  if (h->in_ready) (void)hipEventDestroy(h->in_ready);
+  if (h->out_free) (void)hipEventDestroy(h->out_free);
+  if (h->x_h) (void)hipHostFree(h->x_h);
+  if (h->ids_h) (void)hipHostFree(h->ids_h);
+  if (h->w_h) (void)hipHostFree(h->w_h);
+  if (h->out_h) (void)hipHostFree(h->out_h);
+  if (h->out_d) (void)hipFree(h->out_d);
+  ktmi_cpu::engine_destroy(h->eng);
+  delete h;
+}
+
+}  // namespace
+
+using namespace ktmi;
+
+extern "C" {
+
+ktmi_cpu_moe* ktmi_cpu_moe_create(int64_t hidden, int64_t inter, int type13, int type2, const ktmi_bank* bank,
+                                  int threads, int64_t max_tokens, int64_t max_top_k) {
+  clear_error();
+  if (!bank || max_tokens < 0 || max_top_k < 0) {
+    set_error("cpu_moe_create: null bank or negative sizes");
+    return nullptr;
+  }
+  const char* err = nullptr;
+  ktmi_cpu::Engine* eng = ktmi_cpu::engine_create(hidden, inter, bank->n_experts, type13, type2,
+                                                  (const uint8_t*)bank->gate, (const uint8_t*)bank->up,
+                                                  (const uint8_t*)bank->down, threads, &err);
+  if (!eng) {
+    set_error("cpu_moe_create: %s", err ? err : "failed");
+    return nullptr;
+  }
+  const int64_t rb13 = row_bytes(hidden, type13), rb2 = row_bytes(inter, type2);
+  if (bank->part_gate != inter * rb13 || bank->part_up != inter * rb13 || bank->part_down != hidden * rb2) {
+    set_error("cpu_moe_create: bank part bytes %lld/%lld/%lld, expected %lld/%lld/%lld", (long long)bank->part_gate,
+              (long long)bank->part_up, (long long)bank->part_down, (long long)(inter * rb13),
+              (long long)(inter * rb13), (long long)(hidden * rb2));
+    ktmi_cpu::engine_destroy(eng);
+    return nullptr;
+  }
+  ktmi_cpu_moe* h = new ktmi_cpu_moe{};
+  h->eng = eng;
+  h->K = hidden;
+  h->max_tokens = max_tokens;
+  h->max_top_k = max_top_k;
+  hipError_t e = hipSuccess;
+  if (max_tokens > 0 && max_top_k > 0) {  // a forward-only engine makes no HIP call
+    const size_t P = (size_t)(max_tokens * max_top_k);
+    e = hipGetDevice(&h->device);
+    if (e == hipSuccess) e = hipHostMalloc((void**)&h->x_h, (size_t)(max_tokens * hidden) * 2, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipHostMalloc((void**)&h->ids_h, P * 4, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipHostMalloc((void**)&h->w_h, P * 4, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipHostMalloc((void**)&h->out_h, (size_t)(max_tokens * hidden) * 2, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipMalloc((void**)&h->out_d, (size_t)(max_tokens * hidden) * 2);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&h->in_ready, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&h->out_free, hipEventDisableTiming);
+  }
+  if (e != hipSuccess) {
+    set_error("cpu_moe_create: %s", hipGetErrorString(e));
+    destroy(h);
+    return nullptr;
+  }
+  if (max_tokens > 0 && max_top_k > 0) h->worker = std::thread(worker_loop, h);
+  return h;
+}
+
+int ktmi_cpu_moe_destroy(ktmi_cpu_moe* h) {
+  clear_error();
+  destroy(h);
+  return KTMI_OK;
+}
+
+int ktmi_cpu_moe_threads(const ktmi_cpu_moe* h) { return h ? ktmi_cpu::engine_threads(h->eng) : 0; }
+
+const char* ktmi_cpu_moe_isa(const ktmi_cpu_moe* h) { return h ? ktmi_cpu::engine_isa(h->eng) : ""; }
+
+int ktmi_cpu_moe_forward(ktmi_cpu_moe* h, int64_t tokens, int64_t top_k, const int32_t* expert_ids,
+                         const float* weights, const void* x_bf16, void* out_bf16) {
+  clear_error();
+  KTMI_REQUIRE(h && tokens >= 0 && top_k >= 1, KTMI_EINVAL, "cpu_moe_forward: tokens %lld top_k %lld",
+               (long long)tokens, (long long)top_k);
+  if (tokens == 0) return KTMI_OK;
+  KTMI_REQUIRE(expert_ids && weights && x_bf16 && out_bf16, KTMI_EINVAL, "cpu_moe_forward: null pointer");
+  {
+    std::lock_guard<std::mutex> g(h->m);
+    KTMI_REQUIRE(h->state == ktmi_cpu_moe::IDLE, KTMI_EINVAL, "cpu_moe_forward: a submitted layer is not synced");
+  }
+  const int rc = ktmi_cpu::engine_forward(h->eng, tokens, top_k, expert_ids, weights, (const uint16_t*)x_bf16,
+                                          (uint16_t*)out_bf16);
+  KTMI_REQUIRE(rc == 0, KTMI_ESPACE, "cpu_moe_forward: out of host memory");
+  return KTMI_OK;
+}
+
+int ktmi_cpu_moe_submit(ktmi_cpu_moe* h, const void* x_bf16, const int32_t* expert_ids, const float* weights,
+                        int64_t tokens, int64_t top_k, void* stream) {
+  clear_error();
+  KTMI_REQUIRE(h && tokens >= 0 && top_k >= 1, KTMI_EINVAL, "cpu_moe_submit: tokens %lld top_k %lld",
+               (long long)tokens, (long long)top_k);
+  KTMI_REQUIRE(tokens <= h->max_tokens && top_k <= h->max_top_k, KTMI_EINVAL,
+               "cpu_moe_submit: %lld tokens x top-%lld beyond the staging of %lld x %lld", (long long)tokens,
+               (long long)top_k, (long long)h->max_tokens, (long long)h->max_top_k);
+  std::unique_lock<std::mutex> g(h->m);
+  KTMI_REQUIRE(h->state == ktmi_cpu_moe::IDLE, KTMI_EINVAL, "cpu_moe_submit: the previous layer is not synced");
+  h->T = tokens;
+  h->k = top_k;
+  if (tokens == 0) {
+    h->rc = 0;
+    h->state = ktmi_cpu_moe::DONE;
+    return KTMI_OK;
+  }
+  KTMI_REQUIRE(x_bf16 && expert_ids && weights, KTMI_EINVAL, "cpu_moe_submit: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  KTMI_HIP_TRY(hipMemcpyAsync(h->x_h, x_bf16, (size_t)(tokens * h->K) * 2, hipMemcpyDeviceToHost, s));
+  KTMI_HIP_TRY(hipMemcpyAsync(h->ids_h, expert_ids, (size_t)(tokens * top_k) * 4, hipMemcpyDeviceToHost, s));
+  KTMI_HIP_TRY(hipMemcpyAsync(h->w_h, weights, (size_t)(tokens * top_k) * 4, hipMemcpyDeviceToHost, s));
+  KTMI_HIP_TRY(hipEventRecord(h->in_ready, s));
+  h->state = ktmi_cpu_moe::SUBMITTED;
+  g.unlock();
+  h->cv.notify_all();
+  return KTMI_OK;
+}
+
+int ktmi_cpu_moe_sync_add(ktmi_cpu_moe* h, void* out_bf16, void* stream) {
+  clear_error();
+  KTMI_REQUIRE(h, KTMI_EINVAL, "cpu_moe_sync_add: null engine");
+  int64_t T;
+  {
+    std::unique_lock<std::mutex> g(h->m);
+    KTMI_REQUIRE(h->state != ktmi_cpu_moe::IDLE, KTMI_EINVAL, "cpu_moe_sync_add: nothing submitted");
+    h->cv.wait(g, [h] { return h->state == ktmi_cpu_moe::DONE; });
+    h->state = ktmi_cpu_moe::IDLE;
+    KTMI_REQUIRE(h->rc == 0, KTMI_EHIP, "cpu_moe_sync_add: the CPU side failed (%d)", h->rc);
+    T = h->T;
+  }
+  if (T == 0) return KTMI_OK;
+  KTMI_REQUIRE(out_bf16 && ((uintptr_t)out_bf16 % 16) == 0, KTMI_EINVAL, "cpu_moe_sync_add: output null or not 16-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+  KTMI_HIP_TRY(hipMemcpyAsync(h->out_d, h->out_h, (size_t)(T * h->K) * 2, hipMemcpyHostToDevice, s));
+  KTMI_HIP_TRY(hipEventRecord(h->out_free, s));
+  h->out_free_pending = true;
+  return ktmi_add_bf16(out_bf16, h->out_d, T * h->K, stream);
+}
+
+}  // extern "C"

@@ -7,9 +7,10 @@ exactly the logical ids it is given (residents arrive as -1); KT_HOT_CPU_PREFIX_
 restores the prefix mask (for comparison only).
 
 `hot_split_apply` is the hot-cache branch of KTEPWrapperMethod.apply (P:10590-10602):
-route once, hand the CPU its ids (cpu_submit), run the GPU method on the slot ids,
-then add the CPU partial (cpu_sync). The CPU expert engine (kt-kernel) is not part of
-this library; callers pass its submit/sync callables.
+route once, hand the CPU its ids, run the GPU method on the slot ids, then add the CPU
+partial. The CPU side is a `kt_cpu_moe.KTCPUExperts` (libktmi's CPU expert engine:
+submit stages the inputs and returns, sync_add adds the output on the stream), or any
+submit / sync callables of the caller's own engine.
 """
 from __future__ import annotations
 
@@ -43,14 +44,21 @@ def mask_cpu_expert_ids(topk_ids: torch.Tensor, num_gpu_experts: int) -> torch.T
     return topk_ids
 
 
-def hot_split_apply(cache, layer_idx: int, gpu_method, layer, dispatch_output, cpu_submit=None, cpu_sync=None):
-    """GPU half on the resident slots + CPU half on the rest; returns hidden [T, K]."""
+def hot_split_apply(cache, layer_idx: int, gpu_method, layer, dispatch_output, cpu_submit=None, cpu_sync=None,
+                    cpu=None):
+    """GPU half on the resident slots + CPU half on the rest; returns hidden [T, K].
+    cpu: a KTCPUExperts for this layer (its bank indexed by logical expert id); or
+    cpu_submit(layer, dispatch_output) / cpu_sync(x) -> the CPU partial."""
     x = dispatch_output.hidden_states
     tk = dispatch_output.topk_output
     slot_ids, cpu_ids = cache.route(layer_idx, tk.topk_ids)
-    if cpu_submit is not None:
+    if cpu is not None:
+        cpu.submit(x, cpu_ids, tk.topk_weights)
+    elif cpu_submit is not None:
         cpu_submit(layer, dispatch_output._replace(topk_output=tk._replace(topk_ids=cpu_ids)))
     out = gpu_method.apply(layer, dispatch_output._replace(topk_output=tk._replace(topk_ids=slot_ids))).hidden_states
-    if cpu_sync is not None:
+    if cpu is not None:
+        out = cpu.sync_add(out.contiguous())
+    elif cpu_sync is not None:
         out = out + cpu_sync(x)
     return out
