@@ -128,6 +128,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-stream", action="store_true", help="skip the streamed-layers leg")
+    ap.add_argument("--no-hybrid", action="store_true", help="skip the GPU + CPU decode leg")
     ap.add_argument("--cpu-tokens", type=int, default=1024, help="tokens of the chunk timed on the CPU")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run an fp32 negate of MIB MiB (reads and writes exactly MIB MiB), the known-size "
@@ -219,6 +220,9 @@ def main():
     if not args.no_stream:
         result["stream"] = bench_stream(P, torch, S, ev, dev)
 
+    if not args.no_hybrid:
+        result["hybrid"] = bench_hybrid(P, torch, S, ev, dev)
+
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(S, w, args.cpu_tokens, T)
 
@@ -258,6 +262,71 @@ def bench_decode(P, torch, S, ev, dev, steps=50, warmup=5):
         res[f"T{T}"] = {"hot_routes": int((slot >= 0).sum()), "unique_experts": uniq, "bytes": nbytes, **out}
         log(f"decode T={T}: {res[f'T{T}']}")
     del copies
+    return res
+
+
+def bench_hybrid(P, torch, S, ev, dev, distinct=16, reps=100, warmup=5):
+    """The whole decode layer of the decode workload (256 experts, 32 hot on the GPU, Q4_K)
+    at 1 / 4 / 16 tokens: the hot routes on the GPU (GEMV mode), the cold ones on the host
+    cores through the library's CPU engine and handoff (submit before the GPU kernels,
+    sync_add after). Per step (host clock, reps steps): GPU half alone, CPU half alone
+    (engine forward on host arrays), and the hybrid layer; the CPU engine's rate is the
+    bytes of the distinct cold experts it read per step. Experts: `distinct` quantised
+    experts copied over the 256 bank rows (every row is its own memory)."""
+    H, L = P.kt_gguf_hot, P._lib
+    import kt_prefill_lend_amd.kt_cpu_moe as CM
+    from kt_prefill_lend_amd.gguf import row_bytes
+
+    w = S.WORKLOADS[DECODE]
+    N, K = w.inter, w.hidden
+    parts = [S.expert_weights(w, e, 0, 16) for e in range(distinct)]
+    gate = torch.from_numpy(np.stack([parts[e % distinct][0][:N].reshape(-1) for e in range(w.experts)])).pin_memory()
+    up = torch.from_numpy(np.stack([parts[e % distinct][0][N:].reshape(-1) for e in range(w.experts)])).pin_memory()
+    down = torch.from_numpy(np.stack([parts[e % distinct][1].reshape(-1) for e in range(w.experts)])).pin_memory()
+    cpu = CM.KTCPUExperts(gate, up, down, K, N, w.types, max_tokens=64, max_top_k=w.top_k)
+    w13, w2 = S.slot_tensors(w)
+    W13, W2 = torch.from_numpy(w13).to(dev), torch.from_numpy(w2).to(dev)
+    desc = H.layer_desc(W13, W2, K, N, w.types[0], w.types[2])
+    exp_bytes = 2 * N * row_bytes(K, w.types[0]) + K * row_bytes(N, w.types[2])
+    res = {"workload": w.name, "cpu_threads": cpu.threads, "cpu_isa": cpu.isa}
+
+    def clock(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / reps
+
+    for T in (1, 4, 16):
+        ids, tw, slot, _ = S.routing(w, T)
+        cold = np.where(slot < 0, ids, -1).astype(np.int32)
+        xb = S.activations(w, T)
+        x = torch.from_numpy(xb.view(np.int16)).to(dev).view(torch.bfloat16)
+        x_h = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16)
+        tw_d, slot_d, cold_d = torch.from_numpy(tw).to(dev), torch.from_numpy(slot).to(dev), torch.from_numpy(cold).to(dev)
+        cold_h, tw_h = torch.from_numpy(cold), torch.from_numpy(tw)
+        out = torch.empty((T, K), dtype=torch.bfloat16, device=dev)
+        ws = torch.empty((L.lib().ktmi_moe_layer_workspace(desc, T, w.top_k, L.MODE_GEMV),), dtype=torch.uint8, device=dev)
+        gpu_ms = clock(lambda: H.moe_layer(desc, x, tw_d, slot_d, L.MODE_GEMV, out, ws))
+        cpu_ms = clock(lambda: cpu.forward(x_h, cold_h, tw_h))
+
+        def hybrid():
+            cpu.submit(x, cold_d, tw_d)
+            H.moe_layer(desc, x, tw_d, slot_d, L.MODE_GEMV, out, ws)
+            cpu.sync_add(out)
+
+        hy_ms = clock(hybrid)
+        n_cold = len(set(cold[cold >= 0].tolist()))
+        r = {"hot_routes": int((slot >= 0).sum()), "cold_routes": int((cold >= 0).sum()), "cold_experts": n_cold,
+             "gpu_ms": round(gpu_ms, 4), "cpu_ms": round(cpu_ms, 4), "hybrid_ms": round(hy_ms, 4),
+             "cpu_GBps": round(n_cold * exp_bytes / (cpu_ms * 1e-3) / 1e9, 1),
+             "overlap": round((gpu_ms + cpu_ms - hy_ms) / max(min(gpu_ms, cpu_ms), 1e-9), 3)}
+        res[f"T{T}"] = r
+        log(f"hybrid T={T}: {r}")
+    cpu.close()
     return res
 
 

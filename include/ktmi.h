@@ -204,7 +204,7 @@ int ktmi_host_free(void* p);
  * (ktmi_bank, host memory that outlives the engine); expert ids index the bank, other ids
  * (-1 for the GPU's residents) add nothing. Types: 8, 12, 14, 21. */
 typedef struct ktmi_cpu_moe ktmi_cpu_moe;
-/* threads <= 0: min(16, host threads). max_tokens x max_top_k sizes the pinned staging
+/* threads <= 0: min(16, host threads) - 1. max_tokens x max_top_k sizes the pinned staging
  * of submit (0 for a forward-only engine). Replaces kt-kernel's MOE construction and
  * KExpertsCPUBuffer (the wrapper's CPU side). NULL on failure. */
 ktmi_cpu_moe* ktmi_cpu_moe_create(int64_t hidden, int64_t inter, int type13, int type2, const ktmi_bank* bank,

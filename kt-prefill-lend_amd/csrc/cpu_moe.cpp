@@ -23,6 +23,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <cmath>
 #include <condition_variable>
 #include <functional>
@@ -418,7 +419,9 @@ DotFn dot_for(int t, bool v) {
 }
 
 // ---- a small persistent thread pool: run(n, fn) calls fn(i) for i in [0, n) on the
-// workers and the calling thread, dynamic order, and returns when all are done
+// workers and the calling thread, dynamic order, and returns when all are done. Workers spin
+// on the job counter for a while after each job (a decode layer runs six short phases back
+// to back) before they sleep on the condition variable.
 class Pool {
  public:
   explicit Pool(int threads) : nw_(threads > 1 ? threads - 1 : 0) {
@@ -427,8 +430,8 @@ class Pool {
   ~Pool() {
     {
       std::lock_guard<std::mutex> g(m_);
-      stop_ = true;
-      ++gen_;
+      stop_.store(true);
+      gen_.fetch_add(1);
     }
     cv_.notify_all();
     for (auto& t : th_) t.join();
@@ -440,57 +443,72 @@ class Pool {
       for (int64_t i = 0; i < n; ++i) fn(i);
       return;
     }
+    fn_ = &fn;
+    n_ = n;
+    next_.store(0, std::memory_order_relaxed);
+    left_.store(nw_, std::memory_order_relaxed);
     {
       std::lock_guard<std::mutex> g(m_);
-      fn_ = &fn;
-      n_ = n;
-      next_.store(0);
-      active_ = nw_;
-      ++gen_;
+      gen_.fetch_add(1, std::memory_order_release);
     }
-    cv_.notify_all();
+    if (sleepers_.load() > 0) cv_.notify_all();
     work();
-    std::unique_lock<std::mutex> g(m_);
-    done_.wait(g, [this] { return active_ == 0; });
+    while (left_.load(std::memory_order_acquire) != 0) _mm_pause();
     fn_ = nullptr;
   }
 
  private:
   void work() {
-    for (int64_t i; (i = next_.fetch_add(1)) < n_;) (*fn_)(i);
+    for (int64_t i; (i = next_.fetch_add(1, std::memory_order_relaxed)) < n_;) (*fn_)(i);
   }
   void loop() {
     uint64_t seen = 0;
     for (;;) {
-      {
+      // spin up to 50 microseconds, then sleep
+      bool got = false;
+      const auto t0 = std::chrono::steady_clock::now();
+      for (int i = 0;; ++i) {
+        if (gen_.load(std::memory_order_acquire) != seen) {
+          got = true;
+          break;
+        }
+        _mm_pause();
+        if ((i & 63) == 63 && std::chrono::steady_clock::now() - t0 > std::chrono::microseconds(50)) break;
+      }
+      if (!got) {
         std::unique_lock<std::mutex> g(m_);
-        cv_.wait(g, [&] { return gen_ != seen; });
-        seen = gen_;
-        if (stop_) return;
+        sleepers_.fetch_add(1);
+        cv_.wait(g, [&] { return gen_.load() != seen; });
+        sleepers_.fetch_sub(1);
       }
+      seen = gen_.load(std::memory_order_acquire);
+      if (stop_.load()) return;
       work();
-      {
-        std::lock_guard<std::mutex> g(m_);
-        if (--active_ == 0) done_.notify_one();
-      }
+      left_.fetch_sub(1, std::memory_order_release);
     }
   }
   int nw_;
   std::vector<std::thread> th_;
   std::mutex m_;
-  std::condition_variable cv_, done_;
+  std::condition_variable cv_;
   const std::function<void(int64_t)>* fn_ = nullptr;
   std::atomic<int64_t> next_{0};
   int64_t n_ = 0;
-  int active_ = 0;
-  uint64_t gen_ = 0;
-  bool stop_ = false;
+  std::atomic<int> left_{0}, sleepers_{0};
+  std::atomic<uint64_t> gen_{0};
+  std::atomic<bool> stop_{false};
 };
 
-int64_t row_block(int64_t rows) {
-  for (int64_t b = 256; b > 32; b /= 2)
-    if (rows % b == 0) return b;
-  return 32;
+// rows per task: the widest of 256 .. 16 dividing `rows` that still gives every thread
+// about four tasks over the active experts (small windows get narrow tasks)
+int64_t row_block(int64_t rows, int64_t experts, int threads) {
+  int64_t best = 16;
+  for (int64_t b = 256; b >= 16; b /= 2) {
+    if (rows % b) continue;
+    best = b;
+    if (experts * (rows / b) >= 4 * threads) break;
+  }
+  return rows % best ? rows : best;
 }
 
 }  // namespace
@@ -523,7 +541,9 @@ Engine* engine_create(int64_t hidden, int64_t inter, int64_t n_experts, int type
   if (hidden % block_of(type13) || inter % block_of(type2) || hidden % 256 || inter % 32)
     return fail("hidden / intermediate are not whole blocks of the weight and activation types");
   if (!gate || !up || !down) return fail("null bank pointer");
-  if (threads <= 0) threads = (int)std::min<unsigned>(16, std::max(1u, std::thread::hardware_concurrency()));
+  // default: 16 host threads at most, one of them left to the thread that drives the GPU
+  if (threads <= 0)
+    threads = (int)std::max<unsigned>(1u, std::min<unsigned>(16, std::max(1u, std::thread::hardware_concurrency())) - 1);
   Engine* e = new Engine(threads);
   e->K = hidden;
   e->N = inter;
@@ -584,7 +604,7 @@ int engine_forward(Engine* e, int64_t T, int64_t top_k, const int32_t* ids, cons
     // 3. gate and up per (active expert, row block)
     e->g.resize((size_t)R * N);
     e->u.resize((size_t)R * N);
-    const int64_t mb = row_block(N), nbn = N / mb;
+    const int64_t mb = row_block(N, (int64_t)active.size(), e->pool.size()), nbn = N / mb;
     e->pool.run((int64_t)active.size() * nbn, [&](int64_t task) {
       const int64_t ex = active[task / nbn], r0 = (task % nbn) * mb;
       const uint8_t* wg = e->gate + (size_t)ex * N * e->rb13;
@@ -607,7 +627,7 @@ int engine_forward(Engine* e, int64_t T, int64_t top_k, const int32_t* ids, cons
     });
     // 5. down per (active expert, row block of hidden), then the merge in route order
     e->y.resize((size_t)R * K);
-    const int64_t kb = row_block(K), nbk = K / kb;
+    const int64_t kb = row_block(K, (int64_t)active.size(), e->pool.size()), nbk = K / kb;
     e->pool.run((int64_t)active.size() * nbk, [&](int64_t task) {
       const int64_t ex = active[task / nbk], c0 = (task % nbk) * kb;
       const uint8_t* wd = e->down + (size_t)ex * K * e->rb2;

@@ -9,7 +9,7 @@ struct Engine;
 
 // Expert banks: gate / up uint8 [E, N rows x row_bytes(K, type13)], down uint8
 // [E, K rows x row_bytes(N, type2)] in host memory, kept alive by the caller.
-// threads <= 0: min(16, hardware threads). Returns nullptr (and a message) on bad input.
+// threads <= 0: min(16, hardware threads) - 1 (one left to the thread driving the GPU). Returns nullptr (and a message) on bad input.
 Engine* engine_create(int64_t hidden, int64_t inter, int64_t n_experts, int type13, int type2, const uint8_t* gate,
                       const uint8_t* up, const uint8_t* down, int threads, const char** err);
 void engine_destroy(Engine* e);

@@ -2,14 +2,18 @@
 // kt-kernel's submit_forward / sync_forward as KTEPWrapperMethod calls them around the GPU
 // method (P:10590-10602) and kt_uva_handoff.submit / sync_add (P:41025-41301).
 //
-// submit(x, ids, weights) on the compute stream: three device->host copies into the
-// engine's pinned staging buffers and an event; the engine's worker thread waits for the
+// submit(x, ids, weights) on the compute stream: one kernel writes them into the engine's
+// pinned staging buffers through their device addresses (the reference's UVA staging,
+// kt_uva_handoff._stage_kernel; one launch instead of three small copies), then an event; the engine's worker thread waits for the
 // event, runs the cold routes on the host cores (cpu_moe.cpp) into a pinned bf16 output.
 // The stream goes on with the GPU's hot experts meanwhile. sync_add(out): the host waits
 // for the worker, then a host->device copy of the CPU output and out = bf16(out + cpu) on
 // the stream (the wrapper's `output + cpu_output`). The pinned output is written again
 // only after that copy has completed (event out_free), so back-to-back layers cannot
 // overwrite it early. One submit is outstanding at a time per engine.
+#include <algorithm>
+#include <atomic>
+#include <chrono>
 #include <condition_variable>
 #include <mutex>
 #include <thread>
@@ -26,34 +30,73 @@ struct ktmi_cpu_moe {
   float* w_h = nullptr;
   uint16_t* out_h = nullptr;
   uint16_t* out_d = nullptr;
+  uint16_t* x_hd = nullptr;  // device addresses of the pinned staging buffers
+  int32_t* ids_hd = nullptr;
+  float* w_hd = nullptr;
   hipEvent_t in_ready = nullptr, out_free = nullptr;
   bool out_free_pending = false;
   std::thread worker;
   std::mutex m;
   std::condition_variable cv;
-  enum State { IDLE, SUBMITTED, DONE } state = IDLE;
+  enum State { IDLE, SUBMITTED, DONE };
+  std::atomic<int> state{IDLE};
   int64_t T = 0, k = 0;
   int rc = 0;
-  bool stop = false;
+  std::atomic<bool> stop{false};
 };
 
 namespace {
 
+// x [T, K] bf16 (16-byte chunks), ids and weights [P] into pinned host memory
+__global__ __launch_bounds__(256) void stage_kernel(const u32x4_t* __restrict__ x, int64_t nx,
+                                                     const int32_t* __restrict__ ids, const float* __restrict__ w,
+                                                     int64_t P, u32x4_t* __restrict__ xh, int32_t* __restrict__ idsh,
+                                                     float* __restrict__ wh) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nx; i += stride) xh[i] = x[i];
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < P; i += stride) {
+    idsh[i] = ids[i];
+    wh[i] = w[i];
+  }
+}
+
+// Wait until pred() holds: spin up to `spin_us` microseconds (a decode layer's handoff is
+// tens of microseconds), then sleep on the engine's condition variable.
+template <typename Pred>
+void wait_for(ktmi_cpu_moe* h, Pred pred, int spin_us) {
+  const auto t0 = std::chrono::steady_clock::now();
+  for (int i = 0;; ++i) {
+    if (pred()) return;
+    _mm_pause();
+    if ((i & 63) == 63 && std::chrono::steady_clock::now() - t0 > std::chrono::microseconds(spin_us)) break;
+  }
+  std::unique_lock<std::mutex> g(h->m);
+  h->cv.wait(g, pred);
+}
+
+// an event wait that polls (a short wait on the stream's staging kernel), then blocks
+int event_wait(hipEvent_t e) {
+  for (int i = 0; i < 256; ++i) {
+    const hipError_t q = hipEventQuery(e);
+    if (q == hipSuccess) return 0;
+    if (q != hipErrorNotReady) return -2;
+    _mm_pause();
+  }
+  return hipEventSynchronize(e) == hipSuccess ? 0 : -2;
+}
+
 void worker_loop(ktmi_cpu_moe* h) {
   (void)hipSetDevice(h->device);
   for (;;) {
-    {
-      std::unique_lock<std::mutex> g(h->m);
-      h->cv.wait(g, [h] { return h->stop || h->state == ktmi_cpu_moe::SUBMITTED; });
-      if (h->stop) return;
-    }
-    int rc = hipEventSynchronize(h->in_ready) == hipSuccess ? 0 : -2;
-    if (rc == 0 && h->out_free_pending) rc = hipEventSynchronize(h->out_free) == hipSuccess ? 0 : -2;
+    wait_for(h, [h] { return h->stop || h->state.load() == ktmi_cpu_moe::SUBMITTED; }, 50);
+    if (h->stop) return;
+    int rc = event_wait(h->in_ready);
+    if (rc == 0 && h->out_free_pending) rc = event_wait(h->out_free);
     if (rc == 0) rc = ktmi_cpu::engine_forward(h->eng, h->T, h->k, h->ids_h, h->w_h, h->x_h, h->out_h);
+    h->rc = rc;
     {
       std::lock_guard<std::mutex> g(h->m);
-      h->rc = rc;
-      h->state = ktmi_cpu_moe::DONE;
+      h->state.store(ktmi_cpu_moe::DONE);
     }
     h->cv.notify_all();
   }
@@ -126,6 +169,9 @@ ktmi_cpu_moe* ktmi_cpu_moe_create(int64_t hidden, int64_t inter, int type13, int
     if (e == hipSuccess) e = hipMalloc((void**)&h->out_d, (size_t)(max_tokens * hidden) * 2);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&h->in_ready, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&h->out_free, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipHostGetDevicePointer((void**)&h->x_hd, h->x_h, 0);
+    if (e == hipSuccess) e = hipHostGetDevicePointer((void**)&h->ids_hd, h->ids_h, 0);
+    if (e == hipSuccess) e = hipHostGetDevicePointer((void**)&h->w_hd, h->w_h, 0);
   }
   if (e != hipSuccess) {
     set_error("cpu_moe_create: %s", hipGetErrorString(e));
@@ -180,11 +226,14 @@ int ktmi_cpu_moe_submit(ktmi_cpu_moe* h, const void* x_bf16, const int32_t* expe
     h->state = ktmi_cpu_moe::DONE;
     return KTMI_OK;
   }
-  KTMI_REQUIRE(x_bf16 && expert_ids && weights, KTMI_EINVAL, "cpu_moe_submit: null pointer");
+  KTMI_REQUIRE(x_bf16 && expert_ids && weights && ((uintptr_t)x_bf16 % 16) == 0, KTMI_EINVAL,
+               "cpu_moe_submit: null pointer or x not 16-byte aligned");
   hipStream_t s = (hipStream_t)stream;
-  KTMI_HIP_TRY(hipMemcpyAsync(h->x_h, x_bf16, (size_t)(tokens * h->K) * 2, hipMemcpyDeviceToHost, s));
-  KTMI_HIP_TRY(hipMemcpyAsync(h->ids_h, expert_ids, (size_t)(tokens * top_k) * 4, hipMemcpyDeviceToHost, s));
-  KTMI_HIP_TRY(hipMemcpyAsync(h->w_h, weights, (size_t)(tokens * top_k) * 4, hipMemcpyDeviceToHost, s));
+  const int64_t nx = tokens * h->K / 8, P = tokens * top_k;  // K is a multiple of 256
+  const int64_t blocks = std::min<int64_t>(((nx > P ? nx : P) + 255) / 256, 1024);
+  stage_kernel<<<(unsigned)blocks, 256, 0, s>>>((const u32x4_t*)x_bf16, nx, expert_ids, weights, P,
+                                                (u32x4_t*)h->x_hd, h->ids_hd, h->w_hd);
+  KTMI_HIP_TRY(hipGetLastError());
   KTMI_HIP_TRY(hipEventRecord(h->in_ready, s));
   h->state = ktmi_cpu_moe::SUBMITTED;
   g.unlock();
@@ -195,15 +244,14 @@ int ktmi_cpu_moe_submit(ktmi_cpu_moe* h, const void* x_bf16, const int32_t* expe
 int ktmi_cpu_moe_sync_add(ktmi_cpu_moe* h, void* out_bf16, void* stream) {
   clear_error();
   KTMI_REQUIRE(h, KTMI_EINVAL, "cpu_moe_sync_add: null engine");
-  int64_t T;
+  KTMI_REQUIRE(h->state.load() != ktmi_cpu_moe::IDLE, KTMI_EINVAL, "cpu_moe_sync_add: nothing submitted");
+  wait_for(h, [h] { return h->state.load() == ktmi_cpu_moe::DONE; }, 20);
   {
-    std::unique_lock<std::mutex> g(h->m);
-    KTMI_REQUIRE(h->state != ktmi_cpu_moe::IDLE, KTMI_EINVAL, "cpu_moe_sync_add: nothing submitted");
-    h->cv.wait(g, [h] { return h->state == ktmi_cpu_moe::DONE; });
-    h->state = ktmi_cpu_moe::IDLE;
-    KTMI_REQUIRE(h->rc == 0, KTMI_EHIP, "cpu_moe_sync_add: the CPU side failed (%d)", h->rc);
-    T = h->T;
+    std::lock_guard<std::mutex> g(h->m);
+    h->state.store(ktmi_cpu_moe::IDLE);
   }
+  KTMI_REQUIRE(h->rc == 0, KTMI_EHIP, "cpu_moe_sync_add: the CPU side failed (%d)", h->rc);
+  const int64_t T = h->T;
   if (T == 0) return KTMI_OK;
   KTMI_REQUIRE(out_bf16 && ((uintptr_t)out_bf16 % 16) == 0, KTMI_EINVAL, "cpu_moe_sync_add: output null or not 16-byte aligned");
   hipStream_t s = (hipStream_t)stream;
