@@ -477,8 +477,12 @@ __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restr
     const int ml = q / CW, c = q % CW;
     if (ml < valid) {
       const u32x4_t v = *(const u32x4_t*)(cs + ml * (CW * 16) + 16 * (c ^ (ml % CW)));
-      const int64_t orow = GATEUP ? (int64_t)(m0 + ml) : (int64_t)perm[m0 + ml];
-      *(u32x4_t*)(out + orow * NI + col0 + 8 * c) = v;
+      if constexpr (GATEUP) {
+        *(u32x4_t*)(out + (int64_t)(m0 + ml) * NI + col0 + 8 * c) = v;  // read back by the down GEMM
+      } else {
+        // Y is read once, by the combine, long after: streamed past the caches
+        __builtin_nontemporal_store(v, (u32x4_t*)(out + (int64_t)perm[m0 + ml] * NI + col0 + 8 * c));
+      }
     }
   }
 }
@@ -498,7 +502,7 @@ __global__ __launch_bounds__(256) void combine_routes(const uint16_t* __restrict
       const int e = slot_ids[p];
       if (e < 0 || e >= S) continue;
       const float wk = bf2f(f2bf(w[p]));
-      const u32x4_t v = *(const u32x4_t*)(Y + p * K + c);
+      const u32x4_t v = __builtin_nontemporal_load((const u32x4_t*)(Y + p * K + c));  // read once
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         a[2 * i] += bf2f(f2bf(bf2f(v[i] & 0xFFFF) * wk));
