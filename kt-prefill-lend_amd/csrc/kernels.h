@@ -26,11 +26,11 @@ int launch_moe_gemv(const uint8_t* xq, int64_t xq_stride, const void* W, int w_i
 void record_stage(int i, hipStream_t stream);
 
 // Fused decode-sized layer (decode_layer.hip): two launches, for up to DEC_MAX_ROUTES
-// routes, DEC_MAX_SLOTS slots and hidden sizes whose q8_1 rows fit DEC_MAX_XQ_LDS four
-// times; the stage-by-stage GEMV sequence covers the rest.
+// routes, DEC_MAX_SLOTS slots and hidden sizes whose q8_1 rows fit DEC_MAX_XQ_LDS; the
+// stage-by-stage GEMV sequence covers the rest.
 constexpr int DEC_MAX_ROUTES = 256;
 constexpr int DEC_MAX_SLOTS = 512;
-constexpr int DEC_MAX_XQ_LDS = 64 * 1024;
+constexpr int DEC_MAX_XQ_LDS = 48 * 1024;
 bool decode_layer_fits(const ktmi_layer* L, int64_t tokens, int64_t top_k);
 int64_t decode_layer_workspace(const ktmi_layer* L, int64_t tokens, int64_t top_k);
 int launch_decode_layer(const ktmi_layer* L, const uint16_t* x, const float* topk_w, const int32_t* slot_ids,
