@@ -351,8 +351,6 @@ __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restr
     constexpr int SUB1 = (SUB + 1) & 3, SUB2 = (SUB + 2) & 3, SUB3 = (SUB + 3) & 3;
     const int sb2 = SUB < 2 ? sb : min(sb + 1, lsb);
     const int sb3 = SUB < 1 ? sb : min(sb + 1, lsb);
-#pragma unroll
-    for (int i = 0; i < FI; ++i) BP::template load<SUB2>(b_row[i], sb2, h, grid_lds, raw[cur][i]);
     if constexpr (SUB == 1) {
 #pragma unroll
       for (int i = 0; i < FI; ++i) BP::load_head(b_row[i], min(sb + 1, lsb), h, head_nxt[i]);
@@ -360,10 +358,11 @@ __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restr
     int anext = abuf + AD - 1;
     if (anext >= AD) anext -= AD;
     const uint8_t* Ab = smem + abuf * A_BYTES;
-    // two regions of two sub-steps; in each: 4 of the direct loads of A(k+3), the reads
-    // of the next sub-steps' activation operands (double-buffered in registers), 32 MFMAs
-    // and one piece of the decode of step k+1, interleaved by the schedule below so the
-    // matrix core never waits for a run of decode or for an LDS read
+    // two regions of two sub-steps; in each: half of the direct loads of A(k+3), the raw
+    // bytes of one piece of step k+2 (raw[cur] held step k, decoded one step ago), the
+    // reads of the next sub-steps' activation operands (double-buffered in registers), 32
+    // MFMAs and one piece of the decode of step k+1, interleaved by the schedule below so
+    // the matrix core never waits for a run of decode, an LDS read or a burst of gathers
     static_assert(FI == 2, "the schedule assumes 2 pieces per step");
     constexpr int NMR = 2 * FI * FJ;       // MFMAs per region
     constexpr int DSR = NMR / (2 * FJ);    // MFMAs per LDS read
@@ -374,6 +373,7 @@ __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restr
     for (int s2 = 0; s2 < 4; s2 += 2) {
       __builtin_amdgcn_sched_barrier(0);
       issue_a(sb3, std::integral_constant<int, SUB3>{}, anext, (s2 / 2) * AJ / 2, (s2 / 2 + 1) * AJ / 2);
+      BP::template load<SUB2>(b_row[s2 / 2], sb2, h, grid_lds, raw[cur][s2 / 2]);
 #pragma unroll
       for (int j = 0; j < FJ; ++j) af[1][j] = *(const bf16x8_t*)(Ab + j * 32 * A_ROW + a_rd[s2 + 1]);
 #pragma unroll
@@ -397,21 +397,25 @@ __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restr
       }
       BP::template decode<SUB1>(SUB == 3 ? head_nxt[s2 / 2] : head[s2 / 2], raw[cur ^ 1][s2 / 2], grid_lds,
                                 wv[cur ^ 1][s2 / 2]);
-      // schedule: the loads first, then 32 x (1 MFMA, 4 VALU), an LDS read after every
-      // other MFMA
+      // schedule: the direct loads first, then 32 x (1 MFMA, 4 VALU), an LDS read after
+      // every other MFMA and one of the raw weight gathers after every other (each
+      // gathers 32 rows' cache lines: in one burst they would hold up the MFMA issue)
       __builtin_amdgcn_sched_group_barrier(0x020, AJ / 2, 0);
 #pragma unroll
       for (int m = 0; m < NMR; ++m) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x002, 128 / NMR, 0);
         if (m % DSR == 0) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        if (m % 2 == 1) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    // A(k+1) has landed once at most the newest AJ VMEM ops (the loads of A(k+3)) are
-    // outstanding
-    static_assert(AJ < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt(wait_vmcnt(AJ));
+    // A(k+1) has landed once at most the VMEM ops issued after it are outstanding: A(k+2),
+    // A(k+3) and the raw bytes of steps k+1 and k+2 (at least NLOAD instructions a piece;
+    // the compiler waits for those register loads itself before their decode)
+    constexpr int NYOUNG = 2 * (AJ + FI * BP::NLOAD);
+    static_assert(NYOUNG < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt(wait_vmcnt(NYOUNG));
     lds_barrier();
     abuf = abuf + 1 == AD ? 0 : abuf + 1;
     if constexpr (SUB == 3) {
