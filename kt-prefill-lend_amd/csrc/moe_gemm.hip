@@ -178,7 +178,9 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_scatter(const int32_t* __re
   }
 }
 
-__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + __expf(-g)) * u; }
+// silu(g) * u with the hardware reciprocal (1 ulp) in place of a division: the gate/up epilogue
+// runs it 128 times a lane with no MFMA work left to hide it behind
+__device__ __forceinline__ float silu_mul(float g, float u) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u; }
 
 // Workgroup barrier for the K loop. The caller has already waited for its own LDS traffic:
 // __syncthreads() would add a workgroup fence that also waits for every outstanding direct
@@ -477,15 +479,27 @@ __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restr
   }
   __syncthreads();
   const int64_t col0 = (int64_t)nt * CCOLS;
-  for (int q = tid; q < BM * CW; q += NTHREADS) {
+  // every output row index of this thread first (the down GEMM's rows scatter through perm:
+  // one round of loads rather than one per store), then the stores, unrolled
+  constexpr int NIT = BM * CW / NTHREADS;
+  static_assert(BM * CW % NTHREADS == 0, "store mapping");
+  int orow[NIT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int ml = (tid + it * NTHREADS) / CW;
+    orow[it] = ml < valid ? (GATEUP ? m0 + ml : perm[m0 + ml]) : -1;
+  }
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int q = tid + it * NTHREADS;
     const int ml = q / CW, c = q % CW;
-    if (ml < valid) {
+    if (orow[it] >= 0) {
       const u32x4_t v = *(const u32x4_t*)(cs + ml * (CW * 16) + 16 * (c ^ (ml % CW)));
       if constexpr (GATEUP) {
-        *(u32x4_t*)(out + (int64_t)(m0 + ml) * NI + col0 + 8 * c) = v;  // read back by the down GEMM
+        *(u32x4_t*)(out + (int64_t)orow[it] * NI + col0 + 8 * c) = v;  // read back by the down GEMM
       } else {
         // Y is read once, by the combine, long after: streamed past the caches
-        __builtin_nontemporal_store(v, (u32x4_t*)(out + (int64_t)perm[m0 + ml] * NI + col0 + 8 * c));
+        __builtin_nontemporal_store(v, (u32x4_t*)(out + (int64_t)orow[it] * NI + col0 + 8 * c));
       }
     }
   }
