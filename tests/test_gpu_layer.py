@@ -80,6 +80,38 @@ def test_gemv_mode_matches_reference_kernel_numerics(dev):
     assert l2 < 4e-3, l2
 
 
+FUSED = [
+    # (workload, tokens, top slot must exceed one 16-route pass): at most 256 routes, so GEMV
+    # mode runs the two fused decode launches; 3 tokens stage every h row in LDS, the larger
+    # windows (240 routes, 138 KB of h) read h from HBM and split the busiest slot's routes
+    # over passes of the gate/up block
+    ("q8_0-h2048-n768-e128-k8-hot16", 3, False),
+    ("q8_0-h2048-n768-e128-k8-hot16", 30, True),
+    ("q4_k+q6_k-h2048-n512-e256-k8-hot40-prefill", 3, False),
+    ("q4_k+q6_k-h2048-n512-e256-k8-hot40-prefill", 30, True),
+    ("iq3_s-h2048-n512-e512-k10-hot48", 3, False),
+    ("iq3_s-h2048-n512-e512-k10-hot48", 24, True),
+]
+
+
+@pytest.mark.parametrize("case", FUSED, ids=[f"{c[0].split('-')[0]}-T{c[1]}" for c in FUSED])
+def test_fused_decode_every_type(dev, case):
+    """The fused decode launches for every weight type (gate/up and down), against the
+    oracle's step-by-step restatement of the reference kernels' numerics."""
+    L, _, _ = _pkg()
+    name, T, multi_pass = case
+    w, xb, tw, slot, w13, w2 = _case(name, T, 512, 256, 8, 32)
+    assert slot.size <= 256
+    per_slot = np.bincount(slot[slot >= 0], minlength=8)
+    assert (per_slot.max() > 16) == multi_pass, per_slot
+    got = R.bf16_to_f32(_run(dev, w, xb, tw, slot, w13, w2, L.MODE_GEMV))
+    exp = R.bf16_to_f32(gemv_layer_oracle(xb, tw, slot, w13, w2, w.types, w.hidden, w.inter))
+    l2, _, _ = R.rel_errors(got, exp)
+    print(f"{name} T={T}: rel L2 vs the reference-kernel sequence {l2:.2e}")
+    assert l2 < 4e-3, l2
+    assert np.all(got[(slot < 0).all(axis=1)] == 0)
+
+
 @pytest.mark.parametrize("mode", ["gemv", "grouped"])
 def test_layer_deterministic(dev, mode):
     L, _, _ = _pkg()
