@@ -43,6 +43,7 @@ constexpr int DEC_MAX_UNITS = 64;    // gate/up: weight units per row
 constexpr int DEC_MCH_MAX = 16;      // member routes per pass of the gate/up block, at most
 constexpr int DEC_XQB = 2 * DEC_THREADS;  // gate/up: q8_1 blocks of x per pass, at most
 constexpr int DEC_XRAW_LDS = 64 * 1024;   // gate/up: the pass's bf16 x rows
+constexpr int DEC_PREQ_TOKENS = 8;        // from this many tokens on, x is quantised by its own launch
 constexpr int DEC_MAX_UNITS2 = 16;   // down: weight units per row
 constexpr int DEC_HL_LDS = 80 * 1024;                   // down: staged q8_1 h rows
 static_assert(DEC_MAX_SLOTS <= DEC_THREADS && DEC_MAX_ROUTES <= DEC_THREADS, "one slot and one route per thread");
@@ -217,14 +218,17 @@ __host__ __device__ constexpr int dec_lpr(int units) { return units >= 16 ? 16 :
 // units j, j+16, ... (UPL of them) of gate row 32g+i and of up row N+32g+i, so every
 // activation read serves both. Every weight unit is loaded into registers before any
 // activation is touched; then the member routes (the routes of the slot, ascending, mch
-// per pass) stream past them.
-template <int TYPE, int UPL>
+// per pass) stream past them. With PREQ, x arrives already as q8_1 rows (xq, quantised once
+// per token by the quantize_q8_1 kernel): every block of a slot would otherwise repeat the
+// quantisation of the slot's tokens, the largest cost of the popular slots' blocks once a
+// window holds more than a few tokens.
+template <int TYPE, int UPL, bool PREQ>
 __global__ __launch_bounds__(DEC_THREADS) void decode_gate_up(const __bf16* __restrict__ x, int K, int N,
                                                                  const int32_t* __restrict__ slot_ids, int top_k,
                                                                  int R, int S, const uint8_t* __restrict__ W13,
                                                                  int w_is_table, int64_t w_stride,
                                                                  uint8_t* __restrict__ hq, int64_t hq_stride,
-                                                                 int mch) {
+                                                                 int mch, const uint8_t* __restrict__ xq) {
   // four units a lane (K above 2048 for the 64-value units) leave no registers for unpacked bits
   using U = std::conditional_t<UPL <= 2, DUnit<TYPE>, Unit<TYPE>>;
   constexpr int LPR = DEC_GLPR;
@@ -237,7 +241,7 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_gate_up(const __bf16* __re
   __shared__ float gu[DEC_MCH_MAX][2 * DEC_RG];
   __shared__ int2 xs_lds[DEC_XQB];  // int8 sums of the q8_1 half-blocks
   // the pass's x rows as they are in HBM (bf16), one 64-piece wave load past the last row
-  __shared__ __attribute__((aligned(16))) uint8_t xraw[DEC_XRAW_LDS + 1024];
+  __shared__ __attribute__((aligned(16))) uint8_t xraw[PREQ ? 16 : DEC_XRAW_LDS + 1024];
   __shared__ uint32_t grid[TYPE == GGML_IQ3_S ? 512 : 1];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int G = N / DEC_RG;
@@ -287,25 +291,44 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_gate_up(const __bf16* __re
   const int KB = Kp / 32;  // q8_1 blocks per row; mch * KB <= DEC_XQB, mch * K * 2 <= DEC_XRAW_LDS
   // x rows of a pass's members: buffer loads straight into LDS (16 bytes a lane, piece q of
   // the pass at xraw + 16 q), then q8_1 from there with 8 lanes per 32-value block. Loops,
-  // not unrolled copies: at decode sizes each block runs through its code about once.
-  const int ppr = K / 8;  // 16-byte pieces per x row
-  const uint32_t x_bytes = (uint32_t)(R / top_k) * (uint32_t)K * 2u;
-  const __amdgpu_buffer_rsrc_t x_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, x_bytes, 0x00020000);
+  // not unrolled copies: at decode sizes each block runs through its code about once. With
+  // PREQ the q8_1 rows themselves are loaded into xq_lds and only their half-block sums
+  // are formed here.
+  const int ppr = PREQ ? xq_row / 16 : K / 8;  // 16-byte pieces per row
+  const int T = R / top_k;
+  const uint32_t x_bytes = PREQ ? (uint32_t)T * (uint32_t)xq_row : (uint32_t)T * (uint32_t)K * 2u;
+  const __amdgpu_buffer_rsrc_t x_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(PREQ ? (void*)xq : (void*)x, (short)0, x_bytes, 0x00020000);
+  uint8_t* xdst = PREQ ? xq_lds : xraw;
   auto load_x = [&](int c0, int nc) {
     const int nq = nc * ppr;
+    const uint32_t row_bytes_x = PREQ ? (uint32_t)xq_row : (uint32_t)K * 2u;
     for (int q0 = wv * 64; q0 < nq; q0 += DEC_THREADS) {  // uniform per wave
       const int q = q0 + lane, m = q / ppr;
-      const uint32_t off = q < nq ? (uint32_t)(mem[c0 + m] / top_k) * (uint32_t)K * 2u + (uint32_t)(q - m * ppr) * 16u : x_bytes;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(x_rsrc, (__attribute__((address_space(3))) void*)(xraw + q0 * 16), 16,
+      const uint32_t off = q < nq ? (uint32_t)(mem[c0 + m] / top_k) * row_bytes_x + (uint32_t)(q - m * ppr) * 16u : x_bytes;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(x_rsrc, (__attribute__((address_space(3))) void*)(xdst + q0 * 16), 16,
                                                (int)off, 0, 0, 0);
     }
   };
   auto quantize_x = [&](int nc) {
-    const int nt = nc * KB * 8;
-    for (int q = tid; q < nt; q += DEC_THREADS) {  // whole 8-lane groups: nt is a multiple of 8
-      const int blk = q >> 3, m = blk / KB, kb = blk - m * KB;
-      const u32x2_t xv = kb * 32 < K ? *(const u32x2_t*)(xraw + (m * K + kb * 32) * 2 + (q & 7) * 8) : u32x2_t{0u, 0u};
-      quantize_q8_1_x8(xv, q & 7, xq_lds + m * xq_row + kb * QB8_1, &xs_lds[blk]);  // blk == m * KB + kb
+    if constexpr (PREQ) {
+      for (int blk = tid; blk < nc * KB; blk += DEC_THREADS) {  // blk == m * KB + kb: row m at m * xq_row
+        const uint32_t* qw = (const uint32_t*)(xq_lds + blk * QB8_1 + 4);
+        int lo = 0, hi = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          lo = dot4(0x01010101u, qw[i], lo);
+          hi = dot4(0x01010101u, qw[4 + i], hi);
+        }
+        xs_lds[blk] = int2{lo, hi};
+      }
+    } else {
+      const int nt = nc * KB * 8;
+      for (int q = tid; q < nt; q += DEC_THREADS) {  // whole 8-lane groups: nt is a multiple of 8
+        const int blk = q >> 3, m = blk / KB, kb = blk - m * KB;
+        const u32x2_t xv = kb * 32 < K ? *(const u32x2_t*)(xraw + (m * K + kb * 32) * 2 + (q & 7) * 8) : u32x2_t{0u, 0u};
+        quantize_q8_1_x8(xv, q & 7, xq_lds + m * xq_row + kb * QB8_1, &xs_lds[blk]);  // blk == m * KB + kb
+      }
     }
   };
   load_x(0, min(mch, nm));
@@ -565,9 +588,9 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_down_combine(const uint8_t
 }
 
 template <int TYPE>
-int launch_gate_up(const __bf16* x, int64_t K, int64_t N, const int32_t* slot_ids, int64_t top_k, int64_t R,
-                   int64_t S, const uint8_t* W13, int w_is_table, int64_t w_stride, uint8_t* hq, int64_t hq_stride,
-                   hipStream_t stream) {
+int launch_gate_up(const __bf16* x, const uint8_t* xq, int64_t K, int64_t N, const int32_t* slot_ids, int64_t top_k,
+                   int64_t R, int64_t S, const uint8_t* W13, int w_is_table, int64_t w_stride, uint8_t* hq,
+                   int64_t hq_stride, hipStream_t stream) {
   const int64_t xq_row = q8_1_row_bytes(K);
   const int64_t units = K / Unit<TYPE>::VALS;  // <= DEC_MAX_UNITS: decode_layer_fits
   const int upl = units <= DEC_GLPR ? 1 : units <= 2 * DEC_GLPR ? 2 : 4;
@@ -575,17 +598,24 @@ int launch_gate_up(const __bf16* x, int64_t K, int64_t N, const int32_t* slot_id
   const int kb = (int)(q8_1_cols_padded(K) / 32);
   if (mch * kb > DEC_XQB) mch = DEC_XQB / kb;
   if (mch * K * 2 > DEC_XRAW_LDS) mch = (int)(DEC_XRAW_LDS / (K * 2));
-  const size_t lds = (size_t)mch * (size_t)xq_row;
+  // the q8_1 rows of x arrive by 64-piece wave loads: room for one past the last row
+  const size_t lds = (size_t)mch * (size_t)xq_row + (xq ? 1024 : 0);
   // one block per (slot, row group) walks all of the slot's routes: splitting them over more
   // blocks re-reads the weights once per extra block, which costs more than it saves at
   // decode sizes. Blocks past the slots with routes exit at once.
   const unsigned nb = (unsigned)(S * (N / DEC_RG));
-#define KTMI_GU(P)                                                                                         \
-  decode_gate_up<TYPE, P><<<nb, DEC_THREADS, lds, stream>>>(x, (int)K, (int)N, slot_ids, (int)top_k, (int)R, \
-                                                             (int)S, W13, w_is_table, w_stride, hq, hq_stride, mch)
-  if (upl == 1) KTMI_GU(1);
-  else if (upl == 2) KTMI_GU(2);
-  else KTMI_GU(4);
+#define KTMI_GU(P, Q)                                                                                         \
+  decode_gate_up<TYPE, P, Q><<<nb, DEC_THREADS, lds, stream>>>(x, (int)K, (int)N, slot_ids, (int)top_k, (int)R, \
+                                                                (int)S, W13, w_is_table, w_stride, hq, hq_stride, mch, xq)
+  if (xq) {
+    if (upl == 1) KTMI_GU(1, true);
+    else if (upl == 2) KTMI_GU(2, true);
+    else KTMI_GU(4, true);
+  } else {
+    if (upl == 1) KTMI_GU(1, false);
+    else if (upl == 2) KTMI_GU(2, false);
+    else KTMI_GU(4, false);
+  }
 #undef KTMI_GU
   static_assert(4 * DEC_GLPR >= DEC_MAX_UNITS, "units per lane");
   KTMI_HIP_TRY(hipGetLastError());
@@ -628,8 +658,10 @@ bool decode_layer_fits(const ktmi_layer* L, int64_t tokens, int64_t top_k) {
          L->hidden / unit_vals(L->type13) <= DEC_MAX_UNITS && L->inter / unit_vals(L->type2) <= DEC_MAX_UNITS2;
 }
 
+// workspace: q8_1(h) [R rows of N] | q8_1(x) [T rows of K] (used from DEC_PREQ_TOKENS tokens on)
 int64_t decode_layer_workspace(const ktmi_layer* L, int64_t tokens, int64_t top_k) {
-  return (tokens * top_k * q8_1_row_bytes(L->inter) + 255) & ~(int64_t)255;
+  auto al = [](int64_t v) { return (v + 255) & ~(int64_t)255; };
+  return al(tokens * top_k * q8_1_row_bytes(L->inter)) + al(tokens * q8_1_row_bytes(L->hidden));
 }
 
 int launch_decode_layer(const ktmi_layer* L, const uint16_t* x, const float* topk_w, const int32_t* slot_ids,
@@ -640,13 +672,21 @@ int launch_decode_layer(const ktmi_layer* L, const uint16_t* x, const float* top
   const uint8_t* W2 = (const uint8_t*)L->w2;
   const int64_t st13 = 2 * N * row_bytes(K, L->type13), st2 = K * row_bytes(N, L->type2);
   record_stage(0, stream);
-  record_stage(1, stream);
   int rc;
+  // x quantised once per token for the larger windows (the gate/up blocks of a slot would
+  // each repeat it); below DEC_PREQ_TOKENS tokens the extra launch costs more than it saves
+  uint8_t* xq = nullptr;
+  if (tokens >= DEC_PREQ_TOKENS) {
+    xq = ws + ((R * hq_stride + 255) & ~(int64_t)255);
+    rc = launch_quantize_q8_1(x, KTMI_BF16, K, tokens, xq, stream);
+    if (rc) return rc;
+  }
+  record_stage(1, stream);
   switch (L->type13) {
-    case GGML_Q8_0: rc = launch_gate_up<GGML_Q8_0>((const __bf16*)x, K, N, slot_ids, top_k, R, S, W13, L->w_is_table, st13, ws, hq_stride, stream); break;
-    case GGML_Q4_K: rc = launch_gate_up<GGML_Q4_K>((const __bf16*)x, K, N, slot_ids, top_k, R, S, W13, L->w_is_table, st13, ws, hq_stride, stream); break;
-    case GGML_Q6_K: rc = launch_gate_up<GGML_Q6_K>((const __bf16*)x, K, N, slot_ids, top_k, R, S, W13, L->w_is_table, st13, ws, hq_stride, stream); break;
-    case GGML_IQ3_S: rc = launch_gate_up<GGML_IQ3_S>((const __bf16*)x, K, N, slot_ids, top_k, R, S, W13, L->w_is_table, st13, ws, hq_stride, stream); break;
+    case GGML_Q8_0: rc = launch_gate_up<GGML_Q8_0>((const __bf16*)x, xq, K, N, slot_ids, top_k, R, S, W13, L->w_is_table, st13, ws, hq_stride, stream); break;
+    case GGML_Q4_K: rc = launch_gate_up<GGML_Q4_K>((const __bf16*)x, xq, K, N, slot_ids, top_k, R, S, W13, L->w_is_table, st13, ws, hq_stride, stream); break;
+    case GGML_Q6_K: rc = launch_gate_up<GGML_Q6_K>((const __bf16*)x, xq, K, N, slot_ids, top_k, R, S, W13, L->w_is_table, st13, ws, hq_stride, stream); break;
+    case GGML_IQ3_S: rc = launch_gate_up<GGML_IQ3_S>((const __bf16*)x, xq, K, N, slot_ids, top_k, R, S, W13, L->w_is_table, st13, ws, hq_stride, stream); break;
     default: set_error("decode layer: ggml type %d has no kernel", L->type13); return KTMI_ETYPE;
   }
   if (rc) return rc;
