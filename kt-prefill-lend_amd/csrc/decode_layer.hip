@@ -213,6 +213,72 @@ __device__ __forceinline__ int lanes_below(uint64_t bal) {
 // lanes per row of the down block: 8, or 16 for rows of 16 units (each lane one unit)
 __host__ __device__ constexpr int dec_lpr(int units) { return units >= 16 ? 16 : 8; }
 
+// The block's slot and its routes: blocks are numbered k * G + g over the slots that have
+// routes (ascending), so block kslot serves the kslot-th of them. Leaves the slot's routes in
+// ascending order in mem[0 .. nm) and returns false (for the whole block) when fewer than
+// kslot + 1 slots have routes. Thread p tests route p (R <= DEC_MAX_ROUTES <= DEC_THREADS).
+__device__ __forceinline__ bool slot_members(const int32_t* __restrict__ slot_ids, int R, int S, int kslot,
+                                             uint8_t* present, int (*wsum)[DEC_WAVES], int* sel, int* mem, int& e,
+                                             int& nm) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  present[tid] = 0;  // DEC_MAX_SLOTS <= DEC_THREADS entries
+  const int sid = tid < R ? slot_ids[tid] : -1;
+  __syncthreads();
+  if (sid >= 0 && sid < S) present[sid] = 1;
+  __syncthreads();
+  const bool pres = present[tid] != 0;
+  const uint64_t pb = __ballot(pres);
+  if (lane == 0) wsum[0][wv] = __popcll(pb);
+  __syncthreads();
+  int before = 0, n_act = 0;
+#pragma unroll
+  for (int k = 0; k < DEC_WAVES; ++k) {
+    before += k < wv ? wsum[0][k] : 0;
+    n_act += wsum[0][k];
+  }
+  if (kslot >= n_act) return false;  // uniform
+  if (pres && before + lanes_below(pb) == kslot) *sel = tid;
+  __syncthreads();
+  e = *sel;
+  const bool hit = sid == e;
+  const uint64_t bal = __ballot(hit);
+  if (lane == 0) wsum[1][wv] = __popcll(bal);
+  __syncthreads();
+  int base = 0;
+  nm = 0;
+#pragma unroll
+  for (int k = 0; k < DEC_WAVES; ++k) {
+    base += k < wv ? wsum[1][k] : 0;
+    nm += wsum[1][k];
+  }
+  if (hit) mem[base + lanes_below(bal)] = tid;
+  __syncthreads();
+  return true;
+}
+
+// silu(g)*u in fp32 with one bf16 rounding from the bf16 GEMV outputs gu[m][0..32) (gate
+// rows) and gu[m][32..64) (up rows), then q8_1 block g of each of the nc members' h rows
+__device__ __forceinline__ void silu_h_q8_1(const float (*gu)[2 * DEC_RG], int nc, const int* mem, uint8_t* hq,
+                                            int64_t hq_stride, int g) {
+  for (int idx = threadIdx.x; idx < nc * 32; idx += DEC_THREADS) {
+    const int m = idx / 32, t = idx % 32;
+    const float gg = gu[m][t], uu = gu[m][DEC_RG + t];
+    const float hv = bf16_round(gg / (1.0f + expf(-gg)) * uu);
+    float amax = fabsf(hv);
+    float sum = hv;
+#pragma unroll
+    for (int mask = 16; mask > 0; mask >>= 1) {
+      amax = fmaxf(amax, __shfl_xor(amax, mask, 32));
+      sum += __shfl_xor(sum, mask, 32);
+    }
+    const float d = amax / 127.0f;
+    const int8_t q = amax == 0.0f ? 0 : (int8_t)roundf(hv / d);
+    uint8_t* blk = hq + (int64_t)mem[m] * hq_stride + g * QB8_1;
+    blk[4 + t] = (uint8_t)q;
+    if (t == 0) *(uint32_t*)blk = (uint32_t)float_to_half_bits(d) | ((uint32_t)float_to_half_bits(sum) << 16);
+  }
+}
+
 // One block per (k-th slot with routes, group g of 32 intermediate rows), numbered k * G + g
 // (G = N / 32 groups): 512 threads = 32 intermediate rows x 16 lanes; lane j of row i holds
 // units j, j+16, ... (UPL of them) of gate row 32g+i and of up row N+32g+i, so every
@@ -246,40 +312,9 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_gate_up(const __bf16* __re
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int G = N / DEC_RG;
   const int kslot = blockIdx.x / G, g = blockIdx.x % G;
-  present[tid] = 0;  // DEC_MAX_SLOTS <= DEC_THREADS entries
   if constexpr (TYPE == GGML_IQ3_S) stage_iq3s_grid(grid);
-  const int sid = tid < R ? slot_ids[tid] : -1;
-  __syncthreads();
-  if (sid >= 0 && sid < S) present[sid] = 1;
-  __syncthreads();
-  // the slots with routes, ascending: this block serves the kslot-th
-  const bool pres = present[tid] != 0;
-  const uint64_t pb = __ballot(pres);
-  if (lane == 0) wsum[0][wv] = __popcll(pb);
-  __syncthreads();
-  int before = 0, n_act = 0;
-#pragma unroll
-  for (int k = 0; k < DEC_WAVES; ++k) {
-    before += k < wv ? wsum[0][k] : 0;
-    n_act += wsum[0][k];
-  }
-  if (kslot >= n_act) return;  // uniform: no slot with routes left for this block
-  if (pres && before + lanes_below(pb) == kslot) sel = tid;
-  __syncthreads();
-  const int e = sel;
-  // the routes of slot e in ascending order (thread p tests route p)
-  const bool hit = sid == e;
-  const uint64_t bal = __ballot(hit);
-  if (lane == 0) wsum[1][wv] = __popcll(bal);
-  __syncthreads();
-  int base = 0, nm = 0;
-#pragma unroll
-  for (int k = 0; k < DEC_WAVES; ++k) {
-    base += k < wv ? wsum[1][k] : 0;
-    nm += wsum[1][k];
-  }
-  if (hit) mem[base + lanes_below(bal)] = tid;
-  __syncthreads();
+  int e, nm;
+  if (!slot_members(slot_ids, R, S, kslot, present, wsum, &sel, mem, e, nm)) return;
   const int64_t rb = row_bytes(K, TYPE);
   const uint8_t* wexp = w_is_table ? (const uint8_t*)((const int64_t*)W13)[e] : W13 + (int64_t)e * w_stride;
   const int i = tid / LPR, j0 = tid % LPR;
@@ -381,24 +416,7 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_gate_up(const __bf16* __re
       }
     }
     __syncthreads();
-    // silu(g)*u in fp32, one bf16 rounding, then q8_1 block g of each member's h row
-    for (int idx = tid; idx < nc * 32; idx += DEC_THREADS) {
-      const int m = idx / 32, t = idx % 32;
-      const float gg = gu[m][t], uu = gu[m][DEC_RG + t];
-      const float hv = bf16_round(gg / (1.0f + expf(-gg)) * uu);
-      float amax = fabsf(hv);
-      float sum = hv;
-#pragma unroll
-      for (int mask = 16; mask > 0; mask >>= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, mask, 32));
-        sum += __shfl_xor(sum, mask, 32);
-      }
-      const float d = amax / 127.0f;
-      const int8_t q = amax == 0.0f ? 0 : (int8_t)roundf(hv / d);
-      uint8_t* blk = hq + (int64_t)mem[c0 + m] * hq_stride + g * QB8_1;
-      blk[4 + t] = (uint8_t)q;
-      if (t == 0) *(uint32_t*)blk = (uint32_t)float_to_half_bits(d) | ((uint32_t)float_to_half_bits(sum) << 16);
-    }
+    silu_h_q8_1(gu, nc, mem + c0, hq, hq_stride, g);
     __syncthreads();
   }
 }
