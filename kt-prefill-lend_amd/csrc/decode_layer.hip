@@ -1,10 +1,12 @@
 // Fused decode-sized hot-expert layer (up to DEC_MAX_ROUTES routes): two launches instead
 // of the six of the stage-by-stage sequence (quantize x, gate/up GEMV, SiLU*mul, quantize h,
-// down GEMV, combine), with the same numerics at every stage boundary:
+// down GEMV, combine) -- three from DEC_PREQ_TOKENS tokens on, where x is quantised by its
+// own launch -- with the same numerics at every stage boundary:
 //
 //   decode_gate_up  block (k-th slot with routes, 32-row group g of the intermediate dim):
 //                   lists the routes of the slot, quantises their tokens' x rows to q8_1 in
-//                   LDS, computes gate rows 32g.. and up rows N+32g.. against them with the
+//                   LDS (or loads the q8_1 rows of x quantised by the launch before),
+//                   computes gate rows 32g.. and up rows N+32g.. against them with the
 //                   GEMV's units, rounds to bf16 (the GEMV output dtype), applies
 //                   silu(g)*u in fp32 with one bf16 rounding (sgl-kernel's silu_and_mul
 //                   contract, call at hot/kt_gguf_hot.py:260) and writes the q8_1 block g of
