@@ -275,7 +275,10 @@ float dot_iq3s_scalar(const uint8_t* w, const uint8_t* xv, int64_t n) {
 }
 
 // ---- AVX-512 VNNI block dot products (same integers, same fp32 order)
-#define KT_VNNI __attribute__((target("avx512f,avx512bw,avx512vl,avx512vnni")))
+#define KT_VNNI __attribute__((target("avx512f,avx512bw,avx512vl,avx512vnni,f16c")))
+
+// fp16 -> fp32 with the F16C instruction (exact, as h2f)
+KT_VNNI inline float h2f_hw(uint16_t h) { return _cvtsh_ss(h); }
 
 KT_VNNI inline int hsum8(__m256i v) {
   __m128i s = _mm_add_epi32(_mm256_castsi256_si128(v), _mm256_extracti128_si256(v, 1));
@@ -295,7 +298,7 @@ KT_VNNI float dot_q80_vnni(const uint8_t* w, const uint8_t* xv, int64_t n) {
     const __m256i xq = _mm256_loadu_si256((const __m256i*)x[b].qs);
     // |q| (unsigned) times x with q's sign: exact for |x| <= 127 (the Q8_0 activation codes)
     const __m256i d = _mm256_dpbusd_epi32(_mm256_setzero_si256(), _mm256_abs_epi8(q), _mm256_sign_epi8(xq, q));
-    acc += h2f(dh) * h2f(x[b].d) * (float)hsum8(d);
+    acc += h2f_hw(dh) * h2f_hw(x[b].d) * (float)hsum8(d);
   }
   return acc;
 }
@@ -311,10 +314,21 @@ KT_VNNI float dot_q4k_vnni(const uint8_t* w, const uint8_t* xv, int64_t n) {
     memcpy(&hm, blk + 2, 2);
     __m256i sv = _mm256_setzero_si256();
     int summ = 0;
+    // the eight 6-bit scales and mins of q4k_scale_min, four bytes at a time: sub-blocks
+    // 0-3 are the low 6 bits of bytes 0-3 (scales) and 4-7 (mins); sub-blocks 4-7 take their
+    // low 4 bits from bytes 8-11 and their high 2 bits from bits 6-7 of bytes 0-3 / 4-7
+    uint32_t w1, w2, w3;
+    memcpy(&w1, blk + 4, 4);
+    memcpy(&w2, blk + 8, 4);
+    memcpy(&w3, blk + 12, 4);
+    const uint32_t scl = w1 & 0x3F3F3F3Fu, mnl = w2 & 0x3F3F3F3Fu;
+    const uint32_t sch = (w3 & 0x0F0F0F0Fu) | ((w1 >> 2) & 0x30303030u);
+    const uint32_t mnh = ((w3 >> 4) & 0x0F0F0F0Fu) | ((w2 >> 2) & 0x30303030u);
     for (int g = 0; g < 4; ++g) {
-      int sc0, m0, sc1, m1;
-      q4k_scale_min(blk + 4, 2 * g, sc0, m0);
-      q4k_scale_min(blk + 4, 2 * g + 1, sc1, m1);
+      const uint32_t scw = g < 2 ? scl : sch, mnw = g < 2 ? mnl : mnh;
+      const int sh = 16 * (g & 1);
+      const int sc0 = (int)((scw >> sh) & 0xFF), sc1 = (int)((scw >> (sh + 8)) & 0xFF);
+      const int m0 = (int)((mnw >> sh) & 0xFF), m1 = (int)((mnw >> (sh + 8)) & 0xFF);
       const __m256i q = _mm256_loadu_si256((const __m256i*)(blk + 16 + 32 * g));
       const __m256i lo = _mm256_and_si256(q, m4), hi = _mm256_and_si256(_mm256_srli_epi16(q, 4), m4);
       const __m256i dl = _mm256_dpbusd_epi32(_mm256_setzero_si256(), lo,
@@ -326,7 +340,7 @@ KT_VNNI float dot_q4k_vnni(const uint8_t* w, const uint8_t* xv, int64_t n) {
       summ += m0 * (x[b].bsums[4 * g] + x[b].bsums[4 * g + 1]) + m1 * (x[b].bsums[4 * g + 2] + x[b].bsums[4 * g + 3]);
     }
     const int sumi = hsum8(sv);
-    acc += h2f(hd) * x[b].d * (float)sumi - h2f(hm) * x[b].d * (float)summ;
+    acc += h2f_hw(hd) * x[b].d * (float)sumi - h2f_hw(hm) * x[b].d * (float)summ;
   }
   return acc;
 }
@@ -365,7 +379,7 @@ KT_VNNI float dot_q6k_vnni(const uint8_t* w, const uint8_t* xv, int64_t n) {
     int corr = 0;
     for (int g = 0; g < 16; ++g) corr += sc[g] * x[b].bsums[g];
     const int sumi = hsum8(sv) - 32 * corr;
-    acc += h2f(hd) * x[b].d * (float)sumi;
+    acc += h2f_hw(hd) * x[b].d * (float)sumi;
   }
   return acc;
 }
@@ -393,7 +407,7 @@ KT_VNNI float dot_iq3s_vnni(const uint8_t* w, const uint8_t* xv, int64_t n) {
       const __m256i d = _mm256_dpbusd_epi32(_mm256_setzero_si256(), g, xs);
       sv = _mm256_add_epi32(sv, _mm256_mullo_epi32(d, _mm256_set1_epi32(ls)));
     }
-    acc += h2f(hd) * x[b].d * (float)hsum8(sv);
+    acc += h2f_hw(hd) * x[b].d * (float)hsum8(sv);
   }
   return acc;
 }
