@@ -313,7 +313,6 @@ KT_VNNI float dot_q4k_vnni(const uint8_t* w, const uint8_t* xv, int64_t n) {
     memcpy(&hd, blk, 2);
     memcpy(&hm, blk + 2, 2);
     __m256i sv = _mm256_setzero_si256();
-    int summ = 0;
     // the eight 6-bit scales and mins of q4k_scale_min, four bytes at a time: sub-blocks
     // 0-3 are the low 6 bits of bytes 0-3 (scales) and 4-7 (mins); sub-blocks 4-7 take their
     // low 4 bits from bytes 8-11 and their high 2 bits from bits 6-7 of bytes 0-3 / 4-7
@@ -325,10 +324,9 @@ KT_VNNI float dot_q4k_vnni(const uint8_t* w, const uint8_t* xv, int64_t n) {
     const uint32_t sch = (w3 & 0x0F0F0F0Fu) | ((w1 >> 2) & 0x30303030u);
     const uint32_t mnh = ((w3 >> 4) & 0x0F0F0F0Fu) | ((w2 >> 2) & 0x30303030u);
     for (int g = 0; g < 4; ++g) {
-      const uint32_t scw = g < 2 ? scl : sch, mnw = g < 2 ? mnl : mnh;
+      const uint32_t scw = g < 2 ? scl : sch;
       const int sh = 16 * (g & 1);
       const int sc0 = (int)((scw >> sh) & 0xFF), sc1 = (int)((scw >> (sh + 8)) & 0xFF);
-      const int m0 = (int)((mnw >> sh) & 0xFF), m1 = (int)((mnw >> (sh + 8)) & 0xFF);
       const __m256i q = _mm256_loadu_si256((const __m256i*)(blk + 16 + 32 * g));
       const __m256i lo = _mm256_and_si256(q, m4), hi = _mm256_and_si256(_mm256_srli_epi16(q, 4), m4);
       const __m256i dl = _mm256_dpbusd_epi32(_mm256_setzero_si256(), lo,
@@ -337,8 +335,12 @@ KT_VNNI float dot_q4k_vnni(const uint8_t* w, const uint8_t* xv, int64_t n) {
                                              _mm256_loadu_si256((const __m256i*)(x[b].qs + 64 * g + 32)));
       sv = _mm256_add_epi32(sv, _mm256_mullo_epi32(dl, _mm256_set1_epi32(sc0)));
       sv = _mm256_add_epi32(sv, _mm256_mullo_epi32(dh, _mm256_set1_epi32(sc1)));
-      summ += m0 * (x[b].bsums[4 * g] + x[b].bsums[4 * g + 1]) + m1 * (x[b].bsums[4 * g + 2] + x[b].bsums[4 * g + 3]);
     }
+    // sum over sub-blocks j of m_j * (bsums[2j] + bsums[2j+1]): each min byte doubled to two
+    // int16 lanes against the 16 int16 bsums (exact in int32)
+    const __m128i mb = _mm_cvtsi64_si128((long long)(((uint64_t)mnh << 32) | mnl));
+    const __m256i mv = _mm256_cvtepu8_epi16(_mm_unpacklo_epi8(mb, mb));
+    const int summ = hsum8(_mm256_madd_epi16(_mm256_loadu_si256((const __m256i*)x[b].bsums), mv));
     const int sumi = hsum8(sv);
     acc += h2f_hw(hd) * x[b].d * (float)sumi - h2f_hw(hm) * x[b].d * (float)summ;
   }
