@@ -414,6 +414,40 @@ KT_VNNI float dot_iq3s_vnni(const uint8_t* w, const uint8_t* xv, int64_t n) {
   return acc;
 }
 
+// Q8_K with AVX-512: the codes, sums and scale of quant_q8k (the first value of largest
+// magnitude sets iscale = -127 / value; iscale * x rounded to nearest even by the current
+// mode, as lrint, then clamped; |iscale * x| <= 127, so the int32 conversion never overflows)
+KT_VNNI void quant_q8k_avx512(const float* x, int64_t n, Q8K* y) {
+  const __m512i lo = _mm512_set1_epi32(-128), hi = _mm512_set1_epi32(127);
+  for (int64_t b = 0; b < n / 256; ++b, x += 256) {
+    __m512 vm = _mm512_setzero_ps();
+    for (int c = 0; c < 16; ++c) vm = _mm512_max_ps(vm, _mm512_abs_ps(_mm512_loadu_ps(x + 16 * c)));
+    const float amax = _mm512_reduce_max_ps(vm);
+    if (amax == 0.f) {
+      memset(&y[b], 0, sizeof(Q8K));
+      continue;
+    }
+    int j = 0;
+    for (int c = 0; c < 16; ++c) {
+      const __mmask16 k = _mm512_cmp_ps_mask(_mm512_abs_ps(_mm512_loadu_ps(x + 16 * c)),
+                                             _mm512_set1_ps(amax), _CMP_EQ_OQ);
+      if (k) {
+        j = 16 * c + __builtin_ctz((unsigned)k);
+        break;
+      }
+    }
+    const float iscale = -127.f / x[j];
+    const __m512 vs = _mm512_set1_ps(iscale);
+    for (int c = 0; c < 16; ++c) {
+      __m512i v = _mm512_cvtps_epi32(_mm512_mul_ps(vs, _mm512_loadu_ps(x + 16 * c)));
+      v = _mm512_min_epi32(_mm512_max_epi32(v, lo), hi);
+      _mm_storeu_si128((__m128i*)(y[b].qs + 16 * c), _mm512_cvtepi32_epi8(v));
+      y[b].bsums[c] = (int16_t)_mm512_reduce_add_epi32(v);
+    }
+    y[b].d = 1.f / iscale;
+  }
+}
+
 using DotFn = float (*)(const uint8_t*, const uint8_t*, int64_t);
 
 // the host has AVX-512 VNNI and KTMI_CPU_ISA does not ask for the portable kernels
@@ -532,6 +566,7 @@ int64_t row_block(int64_t rows, int64_t experts, int threads) {
 struct Engine {
   int64_t K, N, E;
   int t13, t2;
+  bool vnni;
   const uint8_t *gate, *up, *down;
   size_t rb13, rb2, xrb, hrb;
   DotFn dot13, dot2;
@@ -576,10 +611,19 @@ Engine* engine_create(int64_t hidden, int64_t inter, int64_t n_experts, int type
   e->dot13 = dot_for(type13, vnni);
   e->dot2 = dot_for(type2, vnni);
   e->isa = vnni ? "avx512-vnni" : "scalar";
+  e->vnni = vnni;
   return e;
 }
 
 void engine_destroy(Engine* e) { delete e; }
+
+namespace {
+// the activation quantiser of the engine's ISA (identical codes either way)
+void quant(const Engine* e, int t, const float* x, int64_t n, uint8_t* y) {
+  if (e->vnni && is_k(t)) quant_q8k_avx512(x, n, (Q8K*)y);
+  else quant_vd(t, x, n, y);
+}
+}  // namespace
 
 int engine_threads(const Engine* e) { return e->pool.size(); }
 
@@ -615,7 +659,7 @@ int engine_forward(Engine* e, int64_t T, int64_t top_k, const int32_t* ids, cons
       thread_local std::vector<float> f;
       f.resize(K);
       for (int64_t c = 0; c < K; ++c) f[c] = bf2f(x[t * K + c]);
-      quant_vd(e->t13, f.data(), K, e->xq.data() + e->xrb * t);
+      quant(e, e->t13, f.data(), K, e->xq.data() + e->xrb * t);
     });
     // 3. gate and up per (active expert, row block)
     e->g.resize((size_t)R * N);
@@ -639,7 +683,7 @@ int engine_forward(Engine* e, int64_t T, int64_t top_k, const int32_t* ids, cons
       float* a = e->g.data() + (size_t)i * N;
       const float* b = e->u.data() + (size_t)i * N;
       for (int64_t r = 0; r < N; ++r) a[r] = a[r] / (1.f + std::exp(-a[r])) * b[r];
-      quant_vd(e->t2, a, N, e->hq.data() + e->hrb * i);
+      quant(e, e->t2, a, N, e->hq.data() + e->hrb * i);
     });
     // 5. down per (active expert, row block of hidden), then the merge in route order
     e->y.resize((size_t)R * K);
