@@ -7,9 +7,9 @@
 //      magnitude; int8 codes rounded to nearest even; int16 sums per 16) for the K-quants
 //      and IQ3_S, Q8_0 (fp16 d = amax/127) for Q8_0;
 //   3. gate and up rows per expert as int8 block dot products, over (expert, row block)
-//      tasks spread on a thread pool;
-//   4. silu(gate) * up in fp32 (x / (1 + expf(-x)) * up, K:2473), re-quantised to the
-//      down vec-dot type;
+//      tasks spread on a thread pool, each task ending with silu(gate) * up of its rows in
+//      fp32 (x / (1 + expf(-x)) * up, K:2473);
+//   4. h re-quantised to the down vec-dot type;
 //   5. down rows per expert, then per token the fp32 sum over k in route order of
 //      y * w, rounded once to bf16.
 // Within a block, the integer dot products are exact (AVX-512 VNNI `vpdpbusd` when the host
@@ -661,7 +661,7 @@ int engine_forward(Engine* e, int64_t T, int64_t top_k, const int32_t* ids, cons
       for (int64_t c = 0; c < K; ++c) f[c] = bf2f(x[t * K + c]);
       quant(e, e->t13, f.data(), K, e->xq.data() + e->xrb * t);
     });
-    // 3. gate and up per (active expert, row block)
+    // 3. gate and up per (active expert, row block), and silu(gate) * up of those rows (in g)
     e->g.resize((size_t)R * N);
     e->u.resize((size_t)R * N);
     const int64_t mb = row_block(N, (int64_t)active.size(), e->pool.size()), nbn = N / mb;
@@ -676,15 +676,15 @@ int engine_forward(Engine* e, int64_t T, int64_t top_k, const int32_t* ids, cons
           e->g[(size_t)i * N + r] = e->dot13(wg + (size_t)r * e->rb13, xr, K);
           e->u[(size_t)i * N + r] = e->dot13(wu + (size_t)r * e->rb13, xr, K);
         }
+      for (int64_t m = 0; m < e->cnt[ex]; ++m) {
+        float* a = e->g.data() + (size_t)(e->off[ex] + m) * N;
+        const float* b = e->u.data() + (size_t)(e->off[ex] + m) * N;
+        for (int64_t r = r0; r < r0 + mb; ++r) a[r] = a[r] / (1.f + std::exp(-a[r])) * b[r];
+      }
     });
-    // 4. silu(gate) * up, quantised for the down projection
+    // 4. h quantised for the down projection
     e->hq.resize(e->hrb * (size_t)R);
-    e->pool.run(R, [&](int64_t i) {
-      float* a = e->g.data() + (size_t)i * N;
-      const float* b = e->u.data() + (size_t)i * N;
-      for (int64_t r = 0; r < N; ++r) a[r] = a[r] / (1.f + std::exp(-a[r])) * b[r];
-      quant(e, e->t2, a, N, e->hq.data() + e->hrb * i);
-    });
+    e->pool.run(R, [&](int64_t i) { quant(e, e->t2, e->g.data() + (size_t)i * N, N, e->hq.data() + e->hrb * i); });
     // 5. down per (active expert, row block of hidden), then the merge in route order
     e->y.resize((size_t)R * K);
     const int64_t kb = row_block(K, (int64_t)active.size(), e->pool.size()), nbk = K / kb;
