@@ -6,11 +6,12 @@
 // pinned staging buffers through their device addresses (the reference's UVA staging,
 // kt_uva_handoff._stage_kernel; one launch instead of three small copies), then an event; the engine's worker thread waits for the
 // event, runs the cold routes on the host cores (cpu_moe.cpp) into a pinned bf16 output.
-// The stream goes on with the GPU's hot experts meanwhile. sync_add(out): the host waits
-// for the worker, then a host->device copy of the CPU output and out = bf16(out + cpu) on
-// the stream (the wrapper's `output + cpu_output`). The pinned output is written again
-// only after that copy has completed (event out_free), so back-to-back layers cannot
-// overwrite it early. One submit is outstanding at a time per engine.
+// The stream goes on with the GPU's hot experts meanwhile. sync_add(out): the host spins
+// until the worker is done, then out = bf16(out + cpu) on the stream (the wrapper's
+// `output + cpu_output`), the add kernel reading the CPU output from pinned memory through
+// its device address (no separate copy). The pinned output is written again only after
+// that add has completed (event out_free), so back-to-back layers cannot overwrite it
+// early. One submit is outstanding at a time per engine.
 #include <algorithm>
 #include <atomic>
 #include <chrono>
@@ -29,10 +30,10 @@ struct ktmi_cpu_moe {
   int32_t* ids_h = nullptr;
   float* w_h = nullptr;
   uint16_t* out_h = nullptr;
-  uint16_t* out_d = nullptr;
   uint16_t* x_hd = nullptr;  // device addresses of the pinned staging buffers
   int32_t* ids_hd = nullptr;
   float* w_hd = nullptr;
+  uint16_t* out_hd = nullptr;
   hipEvent_t in_ready = nullptr, out_free = nullptr;
   bool out_free_pending = false;
   std::thread worker;
@@ -112,14 +113,13 @@ void destroy(ktmi_cpu_moe* h) {
     h->cv.notify_all();
     h->worker.join();
   }
-  if (h->in_ready || h->x_h || h->out_d) (void)hipSetDevice(h->device);
+  if (h->in_ready || h->x_h) (void)hipSetDevice(h->device);
   if (h->in_ready) (void)hipEventDestroy(h->in_ready);
   if (h->out_free) (void)hipEventDestroy(h->out_free);
   if (h->x_h) (void)hipHostFree(h->x_h);
   if (h->ids_h) (void)hipHostFree(h->ids_h);
   if (h->w_h) (void)hipHostFree(h->w_h);
   if (h->out_h) (void)hipHostFree(h->out_h);
-  if (h->out_d) (void)hipFree(h->out_d);
   ktmi_cpu::engine_destroy(h->eng);
   delete h;
 }
@@ -166,12 +166,12 @@ ktmi_cpu_moe* ktmi_cpu_moe_create(int64_t hidden, int64_t inter, int type13, int
     if (e == hipSuccess) e = hipHostMalloc((void**)&h->ids_h, P * 4, hipHostMallocDefault);
     if (e == hipSuccess) e = hipHostMalloc((void**)&h->w_h, P * 4, hipHostMallocDefault);
     if (e == hipSuccess) e = hipHostMalloc((void**)&h->out_h, (size_t)(max_tokens * hidden) * 2, hipHostMallocDefault);
-    if (e == hipSuccess) e = hipMalloc((void**)&h->out_d, (size_t)(max_tokens * hidden) * 2);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&h->in_ready, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&h->out_free, hipEventDisableTiming);
     if (e == hipSuccess) e = hipHostGetDevicePointer((void**)&h->x_hd, h->x_h, 0);
     if (e == hipSuccess) e = hipHostGetDevicePointer((void**)&h->ids_hd, h->ids_h, 0);
     if (e == hipSuccess) e = hipHostGetDevicePointer((void**)&h->w_hd, h->w_h, 0);
+    if (e == hipSuccess) e = hipHostGetDevicePointer((void**)&h->out_hd, h->out_h, 0);
   }
   if (e != hipSuccess) {
     set_error("cpu_moe_create: %s", hipGetErrorString(e));
@@ -245,7 +245,9 @@ int ktmi_cpu_moe_sync_add(ktmi_cpu_moe* h, void* out_bf16, void* stream) {
   clear_error();
   KTMI_REQUIRE(h, KTMI_EINVAL, "cpu_moe_sync_add: null engine");
   KTMI_REQUIRE(h->state.load() != ktmi_cpu_moe::IDLE, KTMI_EINVAL, "cpu_moe_sync_add: nothing submitted");
-  wait_for(h, [h] { return h->state.load() == ktmi_cpu_moe::DONE; }, 20);
+  // the caller has nothing else to do here: spin through the CPU side's whole duration
+  // (a decode layer's is well under this) rather than pay a wake-up on top of it
+  wait_for(h, [h] { return h->state.load() == ktmi_cpu_moe::DONE; }, 2000);
   {
     std::lock_guard<std::mutex> g(h->m);
     h->state.store(ktmi_cpu_moe::IDLE);
@@ -254,11 +256,13 @@ int ktmi_cpu_moe_sync_add(ktmi_cpu_moe* h, void* out_bf16, void* stream) {
   const int64_t T = h->T;
   if (T == 0) return KTMI_OK;
   KTMI_REQUIRE(out_bf16 && ((uintptr_t)out_bf16 % 16) == 0, KTMI_EINVAL, "cpu_moe_sync_add: output null or not 16-byte aligned");
-  hipStream_t s = (hipStream_t)stream;
-  KTMI_HIP_TRY(hipMemcpyAsync(h->out_d, h->out_h, (size_t)(T * h->K) * 2, hipMemcpyHostToDevice, s));
-  KTMI_HIP_TRY(hipEventRecord(h->out_free, s));
+  // the add reads the CPU result straight from pinned memory (no copy to the device first);
+  // out_free marks when it is done, before the worker may write the next result there
+  const int rc = ktmi_add_bf16(out_bf16, h->out_hd, T * h->K, stream);
+  if (rc) return rc;
+  KTMI_HIP_TRY(hipEventRecord(h->out_free, (hipStream_t)stream));
   h->out_free_pending = true;
-  return ktmi_add_bf16(out_bf16, h->out_d, T * h->K, stream);
+  return KTMI_OK;
 }
 
 }  // extern "C"
