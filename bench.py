@@ -135,8 +135,8 @@ def main():
                          "kernel that scales FETCH_SIZE/WRITE_SIZE counters to bytes")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported (this build has no multi-GPU "
-              f"path: the layer would shard by expert, see DESIGN.md)", file=sys.stderr)
+        print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported (there is no multi-GPU "
+              f"path: the layer would shard by expert, each GPU holding its own range of hot slots)", file=sys.stderr)
         sys.exit(2)
 
     import torch

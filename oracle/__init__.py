@@ -1,7 +1,7 @@
 """CPU oracle for the GPU hot-expert MoE path. TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import,
-call, link or run anything in this directory, and only as the checker (or, for
+call, link or run anything in this directory, and only to check results against (or, for
 cpu_moe.c, as the timed CPU baseline). The product path (kt-prefill-lend_amd/)
 never imports it and fails loudly when its HIP library is missing.
 

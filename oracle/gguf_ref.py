@@ -1,6 +1,6 @@
 """numpy restatement of the reference's hot-expert MoE path. TEST INFRASTRUCTURE ONLY
 (only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it, and only
-as the checker).
+to check results against).
 
 Reference files followed (paths relative to the reference repository; `P:<n>` is line
 n of trees/flash-next-gguf/sglang-v0.5.19-flash-next-gguf.patch):
