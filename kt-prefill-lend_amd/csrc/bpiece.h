@@ -54,6 +54,7 @@ struct BPiece;
 template <>
 struct BPiece<GGML_Q4_K> {
   static constexpr int NLOAD = 1;  // VMEM instructions per load<SUB>, at least
+  static constexpr int VPM = 4;    // VALU instructions the GEMM schedule places after each MFMA
   struct Head { u32x4_t hdr; };  // d, dmin, scales[12]
   struct Raw { u32x4_t q; };
   template <int SUB>
@@ -97,6 +98,7 @@ struct BPiece<GGML_Q4_K> {
 template <>
 struct BPiece<GGML_Q8_0> {
   static constexpr int NLOAD = 3;  // VMEM instructions per load<SUB>, at least
+  static constexpr int VPM = 4;    // VALU instructions the GEMM schedule places after each MFMA
   struct Head {};
   struct Raw { uint32_t w[9]; uint32_t s; };
   template <int SUB>
@@ -135,6 +137,7 @@ struct BPiece<GGML_Q8_0> {
 template <>
 struct BPiece<GGML_Q6_K> {
   static constexpr int NLOAD = 4;  // VMEM instructions per load<SUB>, at least
+  static constexpr int VPM = 6;    // VALU instructions the GEMM schedule places after each MFMA
   // the 20 bytes from the dword below scales[0]: scales[16] and d, s = byte shift
   struct Head { uint32_t w[5]; uint32_t s; };
   struct Raw { uint32_t ql[5], qh[5]; };
@@ -198,6 +201,7 @@ struct BPiece<GGML_Q6_K> {
 template <>
 struct BPiece<GGML_IQ3_S> {
   static constexpr int NLOAD = 4;  // VMEM instructions per load<SUB>, at least
+  static constexpr int VPM = 8;    // VALU instructions the GEMM schedule places after each MFMA
   // d and the 4 scale bytes of the block (dwords below them, realigned at decode)
   struct Head { uint32_t dw, sc0, sc1; uint32_t s; };
   // qs[8] of group ib (3 dwords from below), qh byte's dword, signs[4] (2 dwords from below)

@@ -399,14 +399,16 @@ __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restr
       }
       BP::template decode<SUB1>(SUB == 3 ? head_nxt[s2 / 2] : head[s2 / 2], raw[cur ^ 1][s2 / 2], grid_lds,
                                 wv[cur ^ 1][s2 / 2]);
-      // schedule: the direct loads first, then 32 x (1 MFMA, 4 VALU), an LDS read after
+      // schedule: the direct loads first, then 32 x (1 MFMA, VPM VALU), an LDS read after
       // every other MFMA and one of the raw weight gathers after every other (each
-      // gathers 32 rows' cache lines: in one burst they would hold up the MFMA issue)
+      // gathers 32 rows' cache lines: in one burst they would hold up the MFMA issue).
+      // VPM covers the type's decode (Q4_K and Q8_0 about 3.5 VALU per MFMA, Q6_K 6,
+      // IQ3_S 7): VALU left over would run after the last MFMA with the matrix core idle.
       __builtin_amdgcn_sched_group_barrier(0x020, AJ / 2, 0);
 #pragma unroll
       for (int m = 0; m < NMR; ++m) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 128 / NMR, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, BP::VPM, 0);
         if (m % DSR == 0) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         if (m % 2 == 1) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
       }
