@@ -137,7 +137,7 @@ struct BPiece<GGML_Q8_0> {
 template <>
 struct BPiece<GGML_Q6_K> {
   static constexpr int NLOAD = 4;  // VMEM instructions per load<SUB>, at least
-  static constexpr int VPM = 6;    // VALU instructions the GEMM schedule places after each MFMA
+  static constexpr int VPM = 5;    // VALU instructions the GEMM schedule places after each MFMA
   // the 20 bytes from the dword below scales[0]: scales[16] and d, s = byte shift
   struct Head { uint32_t w[5]; uint32_t s; };
   struct Raw { uint32_t ql[5], qh[5]; };
@@ -182,16 +182,19 @@ struct BPiece<GGML_Q6_K> {
     const float d1a = d * (float)(int8_t)((sa >> (16 * c + h8)) & 0xFF);
     const float d1b = d * (float)(int8_t)((sbw >> (16 * c + h8)) & 0xFF);
     constexpr int hsh = 2 * c;
+    // d1 (q - 32) as fma(d1, q, -32 d1): d1 q - 32 d1 is the exact product, rounded once as
+    // the product itself would be (the bytes convert with one v_cvt_f32_ubyteN each)
+    const float n1a = -32.0f * d1a, n1b = -32.0f * d1b;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t lw = alignbyte(r.ql[i + 1], r.ql[i], s);
       const uint32_t hw = alignbyte(r.qh[i + 1], r.qh[i], s);
       const uint32_t va = (lw & 0x0F0F0F0Fu) | (((hw >> hsh) & 0x03030303u) << 4);
       const uint32_t vb = ((lw >> 4) & 0x0F0F0F0Fu) | (((hw >> (hsh + 4)) & 0x03030303u) << 4);
-      out[2 * i] = f2bf2(d1a * (float)((int)(va & 0xFF) - 32), d1a * (float)((int)((va >> 8) & 0xFF) - 32));
-      out[2 * i + 1] = f2bf2(d1a * (float)((int)((va >> 16) & 0xFF) - 32), d1a * (float)((int)(va >> 24) - 32));
-      out[8 + 2 * i] = f2bf2(d1b * (float)((int)(vb & 0xFF) - 32), d1b * (float)((int)((vb >> 8) & 0xFF) - 32));
-      out[8 + 2 * i + 1] = f2bf2(d1b * (float)((int)((vb >> 16) & 0xFF) - 32), d1b * (float)((int)(vb >> 24) - 32));
+      out[2 * i] = f2bf2(__builtin_fmaf(d1a, (float)(va & 0xFF), n1a), __builtin_fmaf(d1a, (float)((va >> 8) & 0xFF), n1a));
+      out[2 * i + 1] = f2bf2(__builtin_fmaf(d1a, (float)((va >> 16) & 0xFF), n1a), __builtin_fmaf(d1a, (float)(va >> 24), n1a));
+      out[8 + 2 * i] = f2bf2(__builtin_fmaf(d1b, (float)(vb & 0xFF), n1b), __builtin_fmaf(d1b, (float)((vb >> 8) & 0xFF), n1b));
+      out[8 + 2 * i + 1] = f2bf2(__builtin_fmaf(d1b, (float)((vb >> 16) & 0xFF), n1b), __builtin_fmaf(d1b, (float)(vb >> 24), n1b));
     }
   }
   __device__ static int off0(int h) { return 16 * h; }
