@@ -42,7 +42,7 @@ struct GroupedPlan {
   int64_t n_slots;
   int64_t max_tiles;   // upper bound of M tiles over all slots
   // workspace carve-up (byte offsets)
-  int64_t off_counts, off_seg, off_tseg, off_tslot, off_perm, off_h, off_y, total;
+  int64_t off_counts, off_seg, off_tseg, off_tinfo, off_perm, off_h, off_y, total;
 };
 GroupedPlan grouped_plan(int64_t tokens, int64_t top_k, int64_t n_slots, int64_t hidden, int64_t inter);
 int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* topk_w, const int32_t* slot_ids,

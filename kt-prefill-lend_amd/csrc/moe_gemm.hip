@@ -116,11 +116,12 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_scan_chunks(int32_t* __rest
 }
 
 // one block: seg[S+1] (route offsets), tseg[S+1] (tile offsets, tiles of bm routes) and
-// tile_slot[tile] (the slot of each tile)
+// tile_info[tile] = {slot, first sorted route, routes in the tile, 0}: a GEMM block reads its
+// tile's whole description in one load instead of a chain of dependent ones
 __global__ __launch_bounds__(SORT_THREADS) void sort_scan_slots(const int32_t* __restrict__ tot, int S,
                                                                 int32_t* __restrict__ seg,
                                                                 int32_t* __restrict__ tseg,
-                                                                int32_t* __restrict__ tile_slot, int bm) {
+                                                                int4* __restrict__ tile_info, int bm) {
   __shared__ int buf[SORT_THREADS];
   const int t = threadIdx.x;
   // two slots per thread (S <= 512)
@@ -134,8 +135,8 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_scan_slots(const int32_t* _
   if (e0 < S) { seg[e0] = ea; tseg[e0] = eb; }
   if (e1 < S) { seg[e1] = ea + a0; tseg[e1] = eb + b0; }
   if (t == 0) { seg[S] = ta; tseg[S] = tb; }
-  for (int q = 0; q < b0; ++q) tile_slot[eb + q] = e0;
-  for (int q = 0; q < b1; ++q) tile_slot[eb + b0 + q] = e1;
+  for (int q = 0; q < b0; ++q) tile_info[eb + q] = int4{e0, ea + q * bm, min(bm, a0 - q * bm), 0};
+  for (int q = 0; q < b1; ++q) tile_info[eb + b0 + q] = int4{e1, ea + a0 + q * bm, min(bm, a1 - q * bm), 0};
 }
 
 __global__ __launch_bounds__(SORT_THREADS) void sort_scatter(const int32_t* __restrict__ slot_ids, int64_t R, int S,
@@ -226,9 +227,8 @@ __device__ __forceinline__ int lds_slot(int row, int chunk) { return chunk ^ (ro
 template <int TYPE, bool GATEUP>
 __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes,
                                                          const int32_t* __restrict__ perm,
-                                                         const int32_t* __restrict__ seg,
                                                          const int32_t* __restrict__ tseg,
-                                                         const int32_t* __restrict__ tile_slot, int S, int top_k,
+                                                         const int4* __restrict__ tile_info, int S, int top_k,
                                                          const uint8_t* __restrict__ W, int w_is_table,
                                                          int64_t w_expert_stride, int64_t rb, int Kdim, int NI,
                                                          int NT, int64_t nblk, uint16_t* __restrict__ out) {
@@ -244,10 +244,12 @@ __global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restr
   const int mt = (int)((idx / NT) * 8 + (pid & 7));
   const int nt = (int)(idx % NT);
   if ((int64_t)mt * NT + nt >= nblk) return;
-  if (mt >= tseg[S]) return;
-  const int e = tile_slot[mt];
-  const int m0 = seg[e] + (mt - tseg[e]) * BM;
-  const int valid = min(BM, seg[e + 1] - m0);
+  // the tile count and the tile's description in parallel (mt < max_tiles: in bounds; the
+  // entries past the count are stale and unused)
+  const int ntiles = tseg[S];
+  const int4 ti = tile_info[mt];
+  if (mt >= ntiles) return;
+  const int e = ti.x, m0 = ti.y, valid = ti.z;
 
   if constexpr (TYPE == GGML_IQ3_S) stage_iq3s_grid(grid_lds);
 
@@ -537,23 +539,23 @@ __global__ __launch_bounds__(256) void combine_routes(const uint16_t* __restrict
 }
 
 template <int TYPE, bool GATEUP>
-void launch_gemm(dim3 grid, hipStream_t stream, const uint16_t* A_src, uint32_t a_bytes, const int32_t* perm, const int32_t* seg,
-                 const int32_t* tseg, const int32_t* tile_slot, int S, int top_k, const void* W, int w_is_table, int64_t w_expert_stride,
+void launch_gemm(dim3 grid, hipStream_t stream, const uint16_t* A_src, uint32_t a_bytes, const int32_t* perm,
+                 const int32_t* tseg, const int4* tile_info, int S, int top_k, const void* W, int w_is_table, int64_t w_expert_stride,
                  int64_t rb, int Kdim, int NI, int NT, int64_t nblk, uint16_t* out) {
-  grouped_gemm<TYPE, GATEUP><<<grid, NTHREADS, 0, stream>>>(A_src, a_bytes, perm, seg, tseg, tile_slot, S, top_k, (const uint8_t*)W,
+  grouped_gemm<TYPE, GATEUP><<<grid, NTHREADS, 0, stream>>>(A_src, a_bytes, perm, tseg, tile_info, S, top_k, (const uint8_t*)W,
                                                              w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out);
 }
 
 template <bool GATEUP>
 int dispatch_gemm(int type, dim3 grid, hipStream_t stream, const uint16_t* A_src, uint32_t a_bytes,
                   const int32_t* perm,
-                  const int32_t* seg, const int32_t* tseg, const int32_t* tile_slot, int S, int top_k, const void* W, int w_is_table,
+                  const int32_t* tseg, const int4* tile_info, int S, int top_k, const void* W, int w_is_table,
                   int64_t w_expert_stride, int64_t rb, int Kdim, int NI, int NT, int64_t nblk, uint16_t* out) {
   switch (type) {
-    case GGML_Q8_0: launch_gemm<GGML_Q8_0, GATEUP>(grid, stream, A_src, a_bytes, perm, seg, tseg, tile_slot, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
-    case GGML_Q4_K: launch_gemm<GGML_Q4_K, GATEUP>(grid, stream, A_src, a_bytes, perm, seg, tseg, tile_slot, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
-    case GGML_Q6_K: launch_gemm<GGML_Q6_K, GATEUP>(grid, stream, A_src, a_bytes, perm, seg, tseg, tile_slot, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
-    case GGML_IQ3_S: launch_gemm<GGML_IQ3_S, GATEUP>(grid, stream, A_src, a_bytes, perm, seg, tseg, tile_slot, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
+    case GGML_Q8_0: launch_gemm<GGML_Q8_0, GATEUP>(grid, stream, A_src, a_bytes, perm, tseg, tile_info, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
+    case GGML_Q4_K: launch_gemm<GGML_Q4_K, GATEUP>(grid, stream, A_src, a_bytes, perm, tseg, tile_info, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
+    case GGML_Q6_K: launch_gemm<GGML_Q6_K, GATEUP>(grid, stream, A_src, a_bytes, perm, tseg, tile_info, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
+    case GGML_IQ3_S: launch_gemm<GGML_IQ3_S, GATEUP>(grid, stream, A_src, a_bytes, perm, tseg, tile_info, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
     default: set_error("grouped GEMM: ggml type %d has no kernel", type); return KTMI_ETYPE;
   }
   KTMI_HIP_TRY(hipGetLastError());
@@ -574,7 +576,7 @@ GroupedPlan grouped_plan(int64_t tokens, int64_t top_k, int64_t n_slots, int64_t
   P.off_counts = o; o = align256(o + ((nch > 0 ? nch : 1) * n_slots + n_slots) * 4);
   P.off_seg = o; o = align256(o + (n_slots + 1) * 4);
   P.off_tseg = o; o = align256(o + (n_slots + 1) * 4);
-  P.off_tslot = o; o = align256(o + P.max_tiles * 4);
+  P.off_tinfo = o; o = align256(o + P.max_tiles * 16);
   P.off_perm = o; o = align256(o + P.routes * 4);
   P.off_h = o; o = align256(o + P.routes * inter * 2);
   P.off_y = o; o = align256(o + P.routes * hidden * 2);
@@ -600,7 +602,7 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
   int32_t* seg = (int32_t*)(ws + P.off_seg);
   int32_t* tseg = (int32_t*)(ws + P.off_tseg);
   int32_t* perm = (int32_t*)(ws + P.off_perm);
-  int32_t* tile_slot = (int32_t*)(ws + P.off_tslot);
+  int4* tile_info = (int4*)(ws + P.off_tinfo);
   uint16_t* H = (uint16_t*)(ws + P.off_h);
   uint16_t* Y = (uint16_t*)(ws + P.off_y);
   const int64_t nch = (R + CHW - 1) / CHW;
@@ -609,7 +611,7 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
   record_stage(0, stream);
   sort_count<<<sblocks, SORT_THREADS, 0, stream>>>(slot_ids, R, S, hist, nch);
   sort_scan_chunks<<<S, SORT_THREADS, 0, stream>>>(hist, nch, tot);
-  sort_scan_slots<<<1, SORT_THREADS, 0, stream>>>(tot, S, seg, tseg, tile_slot, BM);
+  sort_scan_slots<<<1, SORT_THREADS, 0, stream>>>(tot, S, seg, tseg, tile_info, BM);
   sort_scatter<<<sblocks, SORT_THREADS, 0, stream>>>(slot_ids, R, S, hist, nch, seg, perm);
   KTMI_HIP_TRY(hipGetLastError());
   record_stage(1, stream);
@@ -618,7 +620,7 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
   const int NT1 = (int)(N / (BNW / 2));
   const int64_t nblk1 = P.max_tiles * NT1;
   dim3 g1((unsigned)((nblk1 + 8 * NT1 - 1) / (8 * NT1) * (8 * NT1)));
-  int rc = dispatch_gemm<true>(L->type13, g1, stream, x, (uint32_t)(tokens * K * 2), perm, seg, tseg, tile_slot, S, (int)top_k, L->w13, L->w_is_table,
+  int rc = dispatch_gemm<true>(L->type13, g1, stream, x, (uint32_t)(tokens * K * 2), perm, tseg, tile_info, S, (int)top_k, L->w13, L->w_is_table,
                                st13, rb13, (int)K, (int)N, NT1, nblk1, H);
   if (rc) return rc;
   record_stage(2, stream);  // no mid stage on this path: SiLU*mul is in the gate/up epilogue
@@ -626,7 +628,7 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
   const int NT2 = (int)(K / BNW);
   const int64_t nblk2 = P.max_tiles * NT2;
   dim3 g2((unsigned)((nblk2 + 8 * NT2 - 1) / (8 * NT2) * (8 * NT2)));
-  rc = dispatch_gemm<false>(L->type2, g2, stream, H, (uint32_t)(R * N * 2), perm, seg, tseg, tile_slot, S, (int)top_k, L->w2, L->w_is_table, st2, rb2,
+  rc = dispatch_gemm<false>(L->type2, g2, stream, H, (uint32_t)(R * N * 2), perm, tseg, tile_info, S, (int)top_k, L->w2, L->w_is_table, st2, rb2,
                             (int)N, (int)K, NT2, nblk2, Y);
   if (rc) return rc;
   record_stage(4, stream);
