@@ -48,6 +48,13 @@ __device__ __forceinline__ uint32_t and_opaque(uint32_t a, uint32_t m) {
   return r;
 }
 
+// (a & m) | (b & ~m) as one v_bfi_b32 (the compiler otherwise spends an AND, an AND and an OR)
+__device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(m), "v"(a), "v"(b));
+  return r;
+}
+
 template <int TYPE>
 struct BPiece;
 
@@ -204,7 +211,7 @@ struct BPiece<GGML_Q6_K> {
 template <>
 struct BPiece<GGML_IQ3_S> {
   static constexpr int NLOAD = 4;  // VMEM instructions per load<SUB>, at least
-  static constexpr int VPM = 8;    // VALU instructions the GEMM schedule places after each MFMA
+  static constexpr int VPM = 7;    // VALU instructions the GEMM schedule places after each MFMA
   // d and the 4 scale bytes of the block (dwords below them, realigned at decode)
   struct Head { uint32_t dw, sc0, sc1; uint32_t s; };
   // qs[8] of group ib (3 dwords from below), qh byte's dword, signs[4] (2 dwords from below)
@@ -248,23 +255,22 @@ struct BPiece<GGML_IQ3_S> {
     const uint32_t nib = (scw >> (8 * (ib >> 1) + 4 * (ib & 1))) & 15;
     const uint32_t dbits = (hd.dw >> (8 * s)) & 0xFFFF;
     const float db = half_bits_to_float(dbits) * (float)(1 + 2 * (int)nib);
+    // value j of group k takes sign bit 4k + j of sg: (sign ? -v : v) with v = db * grid byte
+    // (whose sign bit is db's, zero included) has the sign bit sg[4k + j] XOR sign(db), so the
+    // sign goes in with one shift and one bitfield insert
+    const uint32_t sgx = sg ^ (uint32_t)((int32_t)__float_as_uint(db) >> 31);
 #pragma unroll
-    for (int l = 0; l < 4; ++l) {
-      const uint32_t sbits = (sg >> (8 * l)) & 0xFF;
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t qsb = ((k < 4 ? qs0 : qs1) >> (8 * (k & 3))) & 0xFF;
+      const uint32_t g = grid[qsb | (((qh >> k) & 1) << 8)];
+      float y[4];
 #pragma unroll
-      for (int sub = 0; sub < 2; ++sub) {
-        const int k = 2 * l + sub;
-        const uint32_t qsb = ((k < 4 ? qs0 : qs1) >> (8 * (k & 3))) & 0xFF;
-        const uint32_t g = grid[qsb | (((qh >> k) & 1) << 8)];
-        float y[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float v = db * (float)((g >> (8 * j)) & 0xFF);
-          y[j] = ((sbits >> (4 * sub + j)) & 1) ? -v : v;
-        }
-        out[2 * k] = f2bf2(y[0], y[1]);
-        out[2 * k + 1] = f2bf2(y[2], y[3]);
+      for (int j = 0; j < 4; ++j) {
+        const float v = db * (float)((g >> (8 * j)) & 0xFF);
+        y[j] = __uint_as_float(bfi(0x80000000u, sgx << (31 - (4 * k + j)), __float_as_uint(v)));
       }
+      out[2 * k] = f2bf2(y[0], y[1]);
+      out[2 * k + 1] = f2bf2(y[2], y[3]);
     }
   }
   __device__ static int off0(int h) { return 32 * h; }
