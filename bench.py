@@ -128,6 +128,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-stream", action="store_true", help="skip the streamed-layers leg")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other workload shapes (Q8_0 512 tokens, 2K/32K chunks, IQ3_S 16K)")
     ap.add_argument("--no-hybrid", action="store_true", help="skip the GPU + CPU decode leg")
     ap.add_argument("--cpu-tokens", type=int, default=1024, help="tokens of the chunk timed on the CPU")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -214,6 +216,9 @@ def main():
         "cpu_baseline": None,
     }
 
+    if not args.no_configs:
+        result["configs"] = bench_configs(P, torch, S, ev, dev)
+
     if not args.no_decode:
         result["decode"] = bench_decode(P, torch, S, ev, dev)
 
@@ -227,6 +232,41 @@ def main():
         result["cpu_baseline"] = cpu_baseline(S, w, args.cpu_tokens, T)
 
     print(json.dumps(result), flush=True)
+
+
+def bench_configs(P, torch, S, ev, dev, steps=10, warmup=2):
+    """The other prefill-sized workloads, one layer each in the mode the library picks: Q8_0
+    at 512 tokens, the headline shapes at 2048 and 32768 tokens and IQ3_S at 16384. Reports
+    tokens/s and the gate/up and down GEMMs' TFLOP/s against the bf16 MFMA peak (stage
+    times from the event pass)."""
+    H, L = P.kt_gguf_hot, P._lib
+    lib = L.lib()
+    cases = [("q8_0-h2048-n768-e128-k8-hot16", 512), (HEADLINE, 2048), (HEADLINE, 32768),
+             ("iq3_s-h2048-n512-e512-k10-hot48", 16384)]
+    res = {}
+    for name, T in cases:
+        w = S.WORKLOADS[name]
+        ids, tw, slot, _ = S.routing(w, T)
+        x = torch.from_numpy(S.activations(w, T).view(np.int16)).to(dev).view(torch.bfloat16)
+        tw_d, slot_d = torch.from_numpy(tw).to(dev), torch.from_numpy(slot).to(dev)
+        w13, w2 = S.slot_tensors(w)
+        W13, W2 = torch.from_numpy(w13).to(dev), torch.from_numpy(w2).to(dev)
+        desc = H.layer_desc(W13, W2, w.hidden, w.inter, w.types[0], w.types[2])
+        mode = lib.ktmi_moe_layer_mode(desc, T, w.top_k)
+        ms, stages, _ = time_layer(P, torch, [desc], x, tw_d, slot_d, mode, steps, warmup, ev)
+        r_hot = int((slot >= 0).sum())
+        f_gu, f_dn = 4.0 * w.hidden * w.inter * r_hot, 2.0 * w.hidden * w.inter * r_hot
+        rec = {"tokens": T, "mode": "grouped" if mode == L.MODE_GROUPED else "gemv", "hot_routes": r_hot,
+               "ms_per_step": round(ms, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
+               "layer_frac_mfma": round((f_gu + f_dn) / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+        for k, f in (("gate_up", f_gu), ("down", f_dn)):
+            if stages[k] > 0:
+                rec[f"{k}_TFLOPs"] = round(f / (stages[k] * 1e-3) / 1e12, 1)
+                rec[f"{k}_frac_mfma"] = round(f / (stages[k] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)
+        res[f"{name}:T{T}"] = rec
+        log(f"config {name} T={T}: {rec}")
+        del W13, W2, x
+    return res
 
 
 def bench_decode(P, torch, S, ev, dev, steps=50, warmup=5):
