@@ -114,6 +114,8 @@ void destroy(ktmi_cpu_moe* h) {
     h->worker.join();
   }
   if (h->in_ready || h->x_h) (void)hipSetDevice(h->device);
+  // the last sync_add's add kernel may still be reading the pinned output
+  if (h->out_free_pending) (void)hipEventSynchronize(h->out_free);
   if (h->in_ready) (void)hipEventDestroy(h->in_ready);
   if (h->out_free) (void)hipEventDestroy(h->out_free);
   if (h->x_h) (void)hipHostFree(h->x_h);

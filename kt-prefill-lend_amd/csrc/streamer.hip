@@ -63,6 +63,8 @@ void destroy(ktmi_streamer* s) {
   (void)hipSetDevice(s->device);
   if (s->copy) (void)hipStreamSynchronize(s->copy);
   for (int i = 0; i < s->n_slots; ++i) {
+    // the compute stream's last group on this slot may still be reading it
+    if (s->released[i]) (void)hipEventSynchronize(s->released[i]);
     if (s->loaded[i]) (void)hipEventDestroy(s->loaded[i]);
     if (s->released[i]) (void)hipEventDestroy(s->released[i]);
     if (s->w13[i]) (void)hipFree(s->w13[i]);
