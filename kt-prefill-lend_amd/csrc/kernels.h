@@ -41,6 +41,8 @@ struct GroupedPlan {
   int64_t routes;      // tokens * top_k
   int64_t n_slots;
   int64_t max_tiles;   // upper bound of M tiles over all slots
+  int fj;              // route fragments of 32 per wave (the kernel's FJ)
+  int64_t bm;          // routes per M tile (32 fj)
   // workspace carve-up (byte offsets)
   int64_t off_counts, off_seg, off_tseg, off_tinfo, off_perm, off_h, off_y, total;
 };

@@ -33,26 +33,26 @@ constexpr int SORT_THREADS = 256;
 constexpr int MAX_SLOTS = 512;
 
 // tile configuration: 4 waves (one per SIMD); wave w owns FI fragments of 32 weight rows
-// and all FJ fragments of 32 routes of the tile: FI x FJ = 16 accumulators of 32 x 32
-// (256 accumulation registers per lane). Tile = BNW weight rows x BM routes (GATEUP: the
-// wave's first FI/2 fragments are gate rows, the others the up rows of the same columns).
-// The weights never touch LDS: each lane loads the raw GGUF bytes of its FI rows and
-// decodes them straight into MFMA operand registers; LDS holds only the activation tile.
+// and all FJ fragments of 32 routes of the tile: FI x FJ accumulators of 32 x 32 (256
+// accumulation registers per lane at FJ = 8). Tile = BNW weight rows x BM routes (GATEUP:
+// the wave's first FI/2 fragments are gate rows, the others the up rows of the same
+// columns). The weights never touch LDS: each lane loads the raw GGUF bytes of its FI rows
+// and decodes them straight into MFMA operand registers; LDS holds only the activation
+// tile. FJ is a kernel parameter: 8 (256-route tiles) for long chunks, 4 (128 routes) when
+// 256-route tiles would leave CUs idle (grouped_fj).
 constexpr int BK = 64;
 constexpr int WN = 4, WM = 1;          // waves over weight rows x waves over routes
 constexpr int NWAVES = WN * WM;
 constexpr int NTHREADS = NWAVES * 64;
-constexpr int FI = 2, FJ = 8;
+constexpr int FI = 2;
 constexpr int BNW = WN * FI * 32;      // weight rows per tile
-constexpr int BM = WM * FJ * 32;       // routes per tile
 constexpr int A_ROW = BK * 2;          // bytes of one activation row per K step
-constexpr int A_BYTES = BM * A_ROW;
+template <int FJ>
+constexpr int tile_m() { return WM * FJ * 32; }  // routes per tile
 // activation buffers: steps k .. k+AD-1 in flight (direct global->LDS loads AD-1 steps
 // ahead); rows of 128 B, 16-byte slots swizzled (lds_slot)
 constexpr int AD = 4;
-constexpr int AJ = A_BYTES / (16 * NTHREADS);  // direct loads per thread per step
-static_assert(AD * A_BYTES + 2048 <= 160 * 1024, "LDS");
-static_assert(AJ % 2 == 0, "A loads are spread over the 2 regions of a step");
+static_assert(AD * tile_m<8>() * A_ROW + 2048 <= 160 * 1024, "LDS");
 
 // ---- route sort by slot. hist is slot-major: hist[e * nch + chunk].
 
@@ -224,14 +224,23 @@ __device__ __forceinline__ int lds_slot(int row, int chunk) { return chunk ^ (ro
 //
 // Epilogue: the accumulators are converted (GATEUP: silu(gate) * up) into a bf16 C tile
 // in LDS, then written out as whole rows.
-template <int TYPE, bool GATEUP>
-__global__ __launch_bounds__(NTHREADS) void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes,
+// 128-route tiles of the light decodes (Q8_0, Q4_K) fit two waves per SIMD (accumulators in
+// VGPRs, 256 registers a lane), so two blocks share a CU; Q6_K and IQ3_S would spill there
+template <int TYPE, bool GATEUP, int FJ>
+constexpr int gemm_waves_per_simd() { return FJ == 8 || TYPE == GGML_Q6_K || TYPE == GGML_IQ3_S ? 1 : 2; }
+
+template <int TYPE, bool GATEUP, int FJ>
+__global__ __launch_bounds__(NTHREADS, (gemm_waves_per_simd<TYPE, GATEUP, FJ>())) void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes,
                                                          const int32_t* __restrict__ perm,
                                                          const int32_t* __restrict__ tseg,
                                                          const int4* __restrict__ tile_info, int S, int top_k,
                                                          const uint8_t* __restrict__ W, int w_is_table,
                                                          int64_t w_expert_stride, int64_t rb, int Kdim, int NI,
                                                          int NT, int64_t nblk, uint16_t* __restrict__ out) {
+  constexpr int BM = tile_m<FJ>();
+  constexpr int A_BYTES = BM * A_ROW;
+  constexpr int AJ = A_BYTES / (16 * NTHREADS);  // direct loads per thread per step
+  static_assert(AJ % 2 == 0, "A loads are spread over the 2 regions of a step");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[AD * A_BYTES];
   __shared__ uint32_t grid_lds[TYPE == GGML_IQ3_S ? 512 : 1];
   using BP = BPiece<TYPE>;
@@ -538,24 +547,36 @@ __global__ __launch_bounds__(256) void combine_routes(const uint16_t* __restrict
   }
 }
 
-template <int TYPE, bool GATEUP>
+template <int TYPE, bool GATEUP, int FJ>
 void launch_gemm(dim3 grid, hipStream_t stream, const uint16_t* A_src, uint32_t a_bytes, const int32_t* perm,
                  const int32_t* tseg, const int4* tile_info, int S, int top_k, const void* W, int w_is_table, int64_t w_expert_stride,
                  int64_t rb, int Kdim, int NI, int NT, int64_t nblk, uint16_t* out) {
-  grouped_gemm<TYPE, GATEUP><<<grid, NTHREADS, 0, stream>>>(A_src, a_bytes, perm, tseg, tile_info, S, top_k, (const uint8_t*)W,
+  grouped_gemm<TYPE, GATEUP, FJ><<<grid, NTHREADS, 0, stream>>>(A_src, a_bytes, perm, tseg, tile_info, S, top_k, (const uint8_t*)W,
                                                              w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out);
 }
 
+template <bool GATEUP, int TYPE>
+void launch_fj(int fj, dim3 grid, hipStream_t stream, const uint16_t* A_src, uint32_t a_bytes, const int32_t* perm,
+               const int32_t* tseg, const int4* tile_info, int S, int top_k, const void* W, int w_is_table,
+               int64_t w_expert_stride, int64_t rb, int Kdim, int NI, int NT, int64_t nblk, uint16_t* out) {
+  if (fj == 8)
+    launch_gemm<TYPE, GATEUP, 8>(grid, stream, A_src, a_bytes, perm, tseg, tile_info, S, top_k, W, w_is_table,
+                                 w_expert_stride, rb, Kdim, NI, NT, nblk, out);
+  else
+    launch_gemm<TYPE, GATEUP, 4>(grid, stream, A_src, a_bytes, perm, tseg, tile_info, S, top_k, W, w_is_table,
+                                 w_expert_stride, rb, Kdim, NI, NT, nblk, out);
+}
+
 template <bool GATEUP>
-int dispatch_gemm(int type, dim3 grid, hipStream_t stream, const uint16_t* A_src, uint32_t a_bytes,
+int dispatch_gemm(int type, int fj, dim3 grid, hipStream_t stream, const uint16_t* A_src, uint32_t a_bytes,
                   const int32_t* perm,
                   const int32_t* tseg, const int4* tile_info, int S, int top_k, const void* W, int w_is_table,
                   int64_t w_expert_stride, int64_t rb, int Kdim, int NI, int NT, int64_t nblk, uint16_t* out) {
   switch (type) {
-    case GGML_Q8_0: launch_gemm<GGML_Q8_0, GATEUP>(grid, stream, A_src, a_bytes, perm, tseg, tile_info, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
-    case GGML_Q4_K: launch_gemm<GGML_Q4_K, GATEUP>(grid, stream, A_src, a_bytes, perm, tseg, tile_info, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
-    case GGML_Q6_K: launch_gemm<GGML_Q6_K, GATEUP>(grid, stream, A_src, a_bytes, perm, tseg, tile_info, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
-    case GGML_IQ3_S: launch_gemm<GGML_IQ3_S, GATEUP>(grid, stream, A_src, a_bytes, perm, tseg, tile_info, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
+    case GGML_Q8_0: launch_fj<GATEUP, GGML_Q8_0>(fj, grid, stream, A_src, a_bytes, perm, tseg, tile_info, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
+    case GGML_Q4_K: launch_fj<GATEUP, GGML_Q4_K>(fj, grid, stream, A_src, a_bytes, perm, tseg, tile_info, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
+    case GGML_Q6_K: launch_fj<GATEUP, GGML_Q6_K>(fj, grid, stream, A_src, a_bytes, perm, tseg, tile_info, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
+    case GGML_IQ3_S: launch_fj<GATEUP, GGML_IQ3_S>(fj, grid, stream, A_src, a_bytes, perm, tseg, tile_info, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
     default: set_error("grouped GEMM: ggml type %d has no kernel", type); return KTMI_ETYPE;
   }
   KTMI_HIP_TRY(hipGetLastError());
@@ -566,12 +587,24 @@ inline int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
 
 }  // namespace
 
+// Route-tile height (FJ fragments of 32 routes): 256 routes when the gate/up GEMM then has
+// about two blocks per CU of the 256, counting every route as hot (R / 256 + S tiles of NT
+// gate/up column tiles), else 128: small chunks trade MFMA work per decoded weight for
+// blocks that fill the chip (Q8_0 at 512 tokens: 0.106 -> 0.087 ms; Q4_K/Q6_K at 2048
+// tokens: 0.204 -> 0.170 ms). 64-route tiles measured slower than either.
+int grouped_fj(int64_t routes, int64_t n_slots, int64_t inter) {
+  const int64_t nt13 = inter / (BNW / 2);
+  return (routes / 256 + n_slots) * nt13 >= 2 * 256 ? 8 : 4;
+}
+
 GroupedPlan grouped_plan(int64_t tokens, int64_t top_k, int64_t n_slots, int64_t hidden, int64_t inter) {
   GroupedPlan P{};
   P.routes = tokens * top_k;
   P.n_slots = n_slots;
+  P.fj = grouped_fj(P.routes, n_slots, inter);
+  P.bm = 32 * WM * P.fj;
   const int64_t nch = (P.routes + CHW - 1) / CHW;
-  P.max_tiles = (P.routes + BM - 1) / BM + n_slots;
+  P.max_tiles = (P.routes + P.bm - 1) / P.bm + n_slots;
   int64_t o = 0;
   P.off_counts = o; o = align256(o + ((nch > 0 ? nch : 1) * n_slots + n_slots) * 4);
   P.off_seg = o; o = align256(o + (n_slots + 1) * 4);
@@ -611,7 +644,7 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
   record_stage(0, stream);
   sort_count<<<sblocks, SORT_THREADS, 0, stream>>>(slot_ids, R, S, hist, nch);
   sort_scan_chunks<<<S, SORT_THREADS, 0, stream>>>(hist, nch, tot);
-  sort_scan_slots<<<1, SORT_THREADS, 0, stream>>>(tot, S, seg, tseg, tile_info, BM);
+  sort_scan_slots<<<1, SORT_THREADS, 0, stream>>>(tot, S, seg, tseg, tile_info, (int)P.bm);
   sort_scatter<<<sblocks, SORT_THREADS, 0, stream>>>(slot_ids, R, S, hist, nch, seg, perm);
   KTMI_HIP_TRY(hipGetLastError());
   record_stage(1, stream);
@@ -620,7 +653,7 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
   const int NT1 = (int)(N / (BNW / 2));
   const int64_t nblk1 = P.max_tiles * NT1;
   dim3 g1((unsigned)((nblk1 + 8 * NT1 - 1) / (8 * NT1) * (8 * NT1)));
-  int rc = dispatch_gemm<true>(L->type13, g1, stream, x, (uint32_t)(tokens * K * 2), perm, tseg, tile_info, S, (int)top_k, L->w13, L->w_is_table,
+  int rc = dispatch_gemm<true>(L->type13, P.fj, g1, stream, x, (uint32_t)(tokens * K * 2), perm, tseg, tile_info, S, (int)top_k, L->w13, L->w_is_table,
                                st13, rb13, (int)K, (int)N, NT1, nblk1, H);
   if (rc) return rc;
   record_stage(2, stream);  // no mid stage on this path: SiLU*mul is in the gate/up epilogue
@@ -628,7 +661,7 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
   const int NT2 = (int)(K / BNW);
   const int64_t nblk2 = P.max_tiles * NT2;
   dim3 g2((unsigned)((nblk2 + 8 * NT2 - 1) / (8 * NT2) * (8 * NT2)));
-  rc = dispatch_gemm<false>(L->type2, g2, stream, H, (uint32_t)(R * N * 2), perm, tseg, tile_info, S, (int)top_k, L->w2, L->w_is_table, st2, rb2,
+  rc = dispatch_gemm<false>(L->type2, P.fj, g2, stream, H, (uint32_t)(R * N * 2), perm, tseg, tile_info, S, (int)top_k, L->w2, L->w_is_table, st2, rb2,
                             (int)N, (int)K, NT2, nblk2, Y);
   if (rc) return rc;
   record_stage(4, stream);
