@@ -3,7 +3,7 @@
 Host-side mirror of the reference's plugin modules (kt_gguf_hot, kt_gguf_moe_multi,
 kt_hot_cache, kt_gguf_dequant, the KT wrapper's CPU-mask hook) over the C ABI of
 lib/libktmi.so (include/ktmi.h): hand-written HIP kernels for the dequant, the route
-lookup and sort, the int8 decode GEMV, the dequant-in-LDS bf16 MFMA grouped GEMMs with
+lookup and sort, the int8 decode GEMV, the bf16 MFMA grouped GEMMs that dequantise in registers, with
 fused SiLU*mul, and the deterministic weighted combine.
 
 The directory name is not a Python identifier; load it as `kt_prefill_lend_amd` with

@@ -9,7 +9,7 @@ Gate and up must share a type.
 `KTGGUFHotExpertsMethod.apply(layer, dispatch_output)` computes this rank's GPU half of a
 MoE layer in one native call (ktmi_moe_layer): decode-sized route counts take the int8
 GEMV over raw blocks (the reference's window kernel), larger ones sort the routes by slot
-and run the dequant-in-LDS bf16 MFMA grouped GEMMs; the weighted top-k combine is the
+and run the bf16 MFMA grouped GEMMs (GGUF blocks dequantised in registers); the weighted top-k combine is the
 reference's _combine order in both. Routes with slot id -1 (experts on the CPU) add
 nothing. KT_HOT_LAYER_MODE=auto|gemv|grouped overrides the choice.
 
