@@ -1,6 +1,6 @@
 // Grouped hot-expert MoE for prefill chunks (gfx950: wave64, bf16 MFMA, 160 KB LDS).
 //
-//   1. sort_count / sort_scan / sort_scatter: a stable counting sort of the routes by
+//   1. sort_count / sort_scan_chunks / sort_scatter: a stable counting sort of the routes by
 //      slot (ascending route index inside a slot, cold routes dropped). Each wave owns a
 //      chunk of CHW consecutive routes; per-chunk histograms are scanned per slot, so
 //      every route's position is a pure function of the ids: no host sync, no atomics
@@ -115,39 +115,42 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_scan_chunks(int32_t* __rest
   if (threadIdx.x == 0) tot[blockIdx.x] = total;
 }
 
-// one block: seg[S+1] (route offsets), tseg[S+1] (tile offsets, tiles of bm routes) and
-// tile_info[tile] = {slot, first sorted route, routes in the tile, 0}: a GEMM block reads its
-// tile's whole description in one load instead of a chain of dependent ones
-__global__ __launch_bounds__(SORT_THREADS) void sort_scan_slots(const int32_t* __restrict__ tot, int S,
-                                                                int32_t* __restrict__ seg,
-                                                                int32_t* __restrict__ tseg,
-                                                                int4* __restrict__ tile_info, int bm) {
-  __shared__ int buf[SORT_THREADS];
-  const int t = threadIdx.x;
-  // two slots per thread (S <= 512)
-  const int e0 = 2 * t, e1 = 2 * t + 1;
-  const int a0 = e0 < S ? tot[e0] : 0, a1 = e1 < S ? tot[e1] : 0;
-  const int b0 = (a0 + bm - 1) / bm, b1 = (a1 + bm - 1) / bm;
-  const int ta = block_scan_256(buf, a0 + a1);
-  const int ea = buf[t];
-  const int tb = block_scan_256(buf, b0 + b1);
-  const int eb = buf[t];
-  if (e0 < S) { seg[e0] = ea; tseg[e0] = eb; }
-  if (e1 < S) { seg[e1] = ea + a0; tseg[e1] = eb + b0; }
-  if (t == 0) { seg[S] = ta; tseg[S] = tb; }
-  for (int q = 0; q < b0; ++q) tile_info[eb + q] = int4{e0, ea + q * bm, min(bm, a0 - q * bm), 0};
-  for (int q = 0; q < b1; ++q) tile_info[eb + b0 + q] = int4{e1, ea + a0 + q * bm, min(bm, a1 - q * bm), 0};
-}
-
+// grid (nch + 3) / 4: wave w of block b scatters the routes of chunk 4b + w to perm. Every
+// block first scans the S slot totals itself (S <= 512, two per thread) for the slots' first
+// sorted positions; block 0 also writes seg[S+1] (route offsets), tseg[S+1] (tile offsets,
+// tiles of bm routes) and tile_info[tile] = {slot, first sorted route, routes in the tile, 0},
+// which a GEMM block reads in one load (no separate launch for the slot scan).
 __global__ __launch_bounds__(SORT_THREADS) void sort_scatter(const int32_t* __restrict__ slot_ids, int64_t R, int S,
                                                              const int32_t* __restrict__ hist, int64_t nch,
-                                                             const int32_t* __restrict__ seg,
+                                                             const int32_t* __restrict__ tot,
+                                                             int32_t* __restrict__ seg, int32_t* __restrict__ tseg,
+                                                             int4* __restrict__ tile_info, int bm,
                                                              int32_t* __restrict__ perm) {
   __shared__ int run[SORT_THREADS / 64][MAX_SLOTS];
+  __shared__ int segl[MAX_SLOTS];
+  __shared__ int buf[SORT_THREADS];
+  const int t = threadIdx.x;
+  const int e0 = 2 * t, e1 = 2 * t + 1;
+  const int a0 = e0 < S ? tot[e0] : 0, a1 = e1 < S ? tot[e1] : 0;
+  const int ta = block_scan_256(buf, a0 + a1);
+  const int ea = buf[t];
+  if (e0 < S) segl[e0] = ea;
+  if (e1 < S) segl[e1] = ea + a0;
+  if (blockIdx.x == 0) {  // uniform
+    const int b0 = (a0 + bm - 1) / bm, b1 = (a1 + bm - 1) / bm;
+    const int tb = block_scan_256(buf, b0 + b1);
+    const int eb = buf[t];
+    if (e0 < S) { seg[e0] = ea; tseg[e0] = eb; }
+    if (e1 < S) { seg[e1] = ea + a0; tseg[e1] = eb + b0; }
+    if (t == 0) { seg[S] = ta; tseg[S] = tb; }
+    for (int q = 0; q < b0; ++q) tile_info[eb + q] = int4{e0, ea + q * bm, min(bm, a0 - q * bm), 0};
+    for (int q = 0; q < b1; ++q) tile_info[eb + b0 + q] = int4{e1, ea + a0 + q * bm, min(bm, a1 - q * bm), 0};
+  }
+  __syncthreads();  // segl
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t ch = (int64_t)blockIdx.x * (SORT_THREADS / 64) + w;
   if (ch >= nch) return;  // whole wave; no block-wide barrier below
-  for (int e = lane; e < S; e += 64) run[w][e] = seg[e] + hist[(int64_t)e * nch + ch];
+  for (int e = lane; e < S; e += 64) run[w][e] = segl[e] + hist[(int64_t)e * nch + ch];
   __builtin_amdgcn_wave_barrier();
   const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   const int64_t p0 = ch * CHW;
@@ -644,8 +647,8 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
   record_stage(0, stream);
   sort_count<<<sblocks, SORT_THREADS, 0, stream>>>(slot_ids, R, S, hist, nch);
   sort_scan_chunks<<<S, SORT_THREADS, 0, stream>>>(hist, nch, tot);
-  sort_scan_slots<<<1, SORT_THREADS, 0, stream>>>(tot, S, seg, tseg, tile_info, (int)P.bm);
-  sort_scatter<<<sblocks, SORT_THREADS, 0, stream>>>(slot_ids, R, S, hist, nch, seg, perm);
+  sort_scatter<<<sblocks, SORT_THREADS, 0, stream>>>(slot_ids, R, S, hist, nch, tot, seg, tseg, tile_info, (int)P.bm,
+                                                     perm);
   KTMI_HIP_TRY(hipGetLastError());
   record_stage(1, stream);
   const int64_t rb13 = row_bytes(K, L->type13), rb2 = row_bytes(N, L->type2);
