@@ -6,7 +6,13 @@ expert intermediate 512, 256 experts, top-8, 40 hot slots, Q4_K gate/up + Q6_K d
 1.1 routing), inputs resident in HBM. A step is one layer forward (route sort, gate/up
 GEMM with SiLU*mul, down GEMM, weighted combine) over the chunk. Prints ONE JSON line.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-decode]
+Besides the headline (`value`, `roofline`, `cpu_baseline`), the line carries the other
+legs: `configs` (Q8_0 512 tokens, 2K and 32K chunks, IQ3_S 16K against the MFMA peak),
+`decode` (1/4/8/16-token layers against HBM), `stream` (four large layers streamed from
+pinned host memory) and `hybrid` (hot routes on the GPU, cold ones on the host cores).
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-configs]
+                    [--no-decode] [--no-stream] [--no-hybrid]
 """
 from __future__ import annotations
 
