@@ -188,3 +188,24 @@ def test_stream_bank_validation_and_threshold(monkeypatch):
     monkeypatch.setattr(SP, "preallocate", lambda *a, **k: "streamer")
     assert SP.stream_prefill_for(N, K, 8, types, 1024) is None
     assert SP.stream_prefill_for(N, K, 8, types, 8192) == "streamer"
+
+
+def test_layer_argument_errors_before_device_work():
+    """The layer entry point rejects bad arguments with a status and a message before it
+    touches the device (the pointers below are never dereferenced): a short workspace,
+    misaligned activations, a forced GEMV mode past its route limit, a chunk past the
+    activations' 4 GiB buffer range."""
+    from kt_prefill_lend_amd import _lib
+
+    L = _lib.lib()
+    d = _lib.ktmi_layer(hidden=2048, inter=512, n_slots=40, type13=12, type2=14, w13=1 << 20, w2=2 << 20)
+    p, big = 1 << 24, 1 << 62
+    need = L.ktmi_moe_layer_workspace(d, 4096, 8, _lib.MODE_GROUPED)
+    rc = L.ktmi_moe_layer(d, p, p, p, 4096, 8, p, p, need - 1, _lib.MODE_GROUPED, 0)
+    assert rc == -4 and b"workspace" in L.ktmi_last_error()
+    rc = L.ktmi_moe_layer(d, p + 8, p, p, 4096, 8, p, p, big, _lib.MODE_GROUPED, 0)
+    assert rc == -1 and b"aligned" in L.ktmi_last_error()
+    rc = L.ktmi_moe_layer(d, p, p, p, 10000, 8, p, p, big, _lib.MODE_GEMV, 0)
+    assert rc == -1 and b"65535" in L.ktmi_last_error()
+    rc = L.ktmi_moe_layer(d, p, p, p, 1 << 20, 8, p, p, big, _lib.MODE_GROUPED, 0)
+    assert rc == -1 and b"4 GiB" in L.ktmi_last_error()
