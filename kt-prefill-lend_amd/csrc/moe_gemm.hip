@@ -206,6 +206,11 @@ constexpr int wait_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) 
 // are free of bank conflicts.
 __device__ __forceinline__ int lds_slot(int row, int chunk) { return chunk ^ (row & 7) ^ ((row >> 3) & 1); }
 
+// 128-route tiles of the light decodes (Q8_0, Q4_K) fit two waves per SIMD (accumulators in
+// VGPRs, 256 registers a lane), so two blocks share a CU; Q6_K and IQ3_S would spill there.
+template <int TYPE, int FJ>
+constexpr int gemm_waves_per_simd() { return FJ == 8 || TYPE == GGML_Q6_K || TYPE == GGML_IQ3_S ? 1 : 2; }
+
 // GATEUP = true : activations = x rows gathered through perm (token = p / top_k),
 //                 Kdim = hidden, weight rows = [gate n0.. ; up NI+n0..], out = H [R, NI]
 //                 sorted rows, silu(gate) * up.
@@ -227,13 +232,9 @@ __device__ __forceinline__ int lds_slot(int row, int chunk) { return chunk ^ (ro
 //
 // Epilogue: the accumulators are converted (GATEUP: silu(gate) * up) into a bf16 C tile
 // in LDS, then written out as whole rows.
-// 128-route tiles of the light decodes (Q8_0, Q4_K) fit two waves per SIMD (accumulators in
-// VGPRs, 256 registers a lane), so two blocks share a CU; Q6_K and IQ3_S would spill there
 template <int TYPE, bool GATEUP, int FJ>
-constexpr int gemm_waves_per_simd() { return FJ == 8 || TYPE == GGML_Q6_K || TYPE == GGML_IQ3_S ? 1 : 2; }
-
-template <int TYPE, bool GATEUP, int FJ>
-__global__ __launch_bounds__(NTHREADS, (gemm_waves_per_simd<TYPE, GATEUP, FJ>())) void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes,
+__global__ __launch_bounds__(NTHREADS, (gemm_waves_per_simd<TYPE, FJ>()))
+void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes,
                                                          const int32_t* __restrict__ perm,
                                                          const int32_t* __restrict__ tseg,
                                                          const int4* __restrict__ tile_info, int S, int top_k,
