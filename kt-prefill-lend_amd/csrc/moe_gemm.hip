@@ -117,9 +117,10 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_scan_chunks(int32_t* __rest
 
 // grid (nch + 3) / 4: wave w of block b scatters the routes of chunk 4b + w to perm. Every
 // block first scans the S slot totals itself (S <= 512, two per thread) for the slots' first
-// sorted positions; block 0 also writes seg[S+1] (route offsets), tseg[S+1] (tile offsets,
-// tiles of bm routes) and tile_info[tile] = {slot, first sorted route, routes in the tile, 0},
-// which a GEMM block reads in one load (no separate launch for the slot scan).
+// sorted positions and first tiles (tiles of bm routes); block 0 writes seg[S+1] (route
+// offsets) and tseg[S+1] (tile offsets), and thread i of the grid writes tile_info[i] =
+// {slot, first sorted route, routes in the tile, 0} for i < tseg[S] (a GEMM block reads its
+// tile in one load; no separate launch for the slot scan).
 __global__ __launch_bounds__(SORT_THREADS) void sort_scatter(const int32_t* __restrict__ slot_ids, int64_t R, int S,
                                                              const int32_t* __restrict__ hist, int64_t nch,
                                                              const int32_t* __restrict__ tot,
@@ -127,26 +128,38 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_scatter(const int32_t* __re
                                                              int4* __restrict__ tile_info, int bm,
                                                              int32_t* __restrict__ perm) {
   __shared__ int run[SORT_THREADS / 64][MAX_SLOTS];
-  __shared__ int segl[MAX_SLOTS];
+  __shared__ int segl[MAX_SLOTS + 1];
+  __shared__ int tsegl[MAX_SLOTS + 1];
   __shared__ int buf[SORT_THREADS];
   const int t = threadIdx.x;
   const int e0 = 2 * t, e1 = 2 * t + 1;
   const int a0 = e0 < S ? tot[e0] : 0, a1 = e1 < S ? tot[e1] : 0;
+  const int b0 = (a0 + bm - 1) / bm, b1 = (a1 + bm - 1) / bm;
   const int ta = block_scan_256(buf, a0 + a1);
   const int ea = buf[t];
-  if (e0 < S) segl[e0] = ea;
-  if (e1 < S) segl[e1] = ea + a0;
-  if (blockIdx.x == 0) {  // uniform
-    const int b0 = (a0 + bm - 1) / bm, b1 = (a1 + bm - 1) / bm;
-    const int tb = block_scan_256(buf, b0 + b1);
-    const int eb = buf[t];
+  const int tb = block_scan_256(buf, b0 + b1);
+  const int eb = buf[t];
+  if (e0 < S) { segl[e0] = ea; tsegl[e0] = eb; }
+  if (e1 < S) { segl[e1] = ea + a0; tsegl[e1] = eb + b0; }
+  if (t == 0) { segl[S] = ta; tsegl[S] = tb; }
+  if (blockIdx.x == 0) {
     if (e0 < S) { seg[e0] = ea; tseg[e0] = eb; }
     if (e1 < S) { seg[e1] = ea + a0; tseg[e1] = eb + b0; }
     if (t == 0) { seg[S] = ta; tseg[S] = tb; }
-    for (int q = 0; q < b0; ++q) tile_info[eb + q] = int4{e0, ea + q * bm, min(bm, a0 - q * bm), 0};
-    for (int q = 0; q < b1; ++q) tile_info[eb + b0 + q] = int4{e1, ea + a0 + q * bm, min(bm, a1 - q * bm), 0};
   }
-  __syncthreads();  // segl
+  __syncthreads();  // segl, tsegl
+  // this thread's tile (if any): its slot is the last e with tsegl[e] <= i (binary search)
+  for (int64_t i = (int64_t)blockIdx.x * SORT_THREADS + t; i < tb; i += (int64_t)gridDim.x * SORT_THREADS) {
+    int lo = 0, hi = S - 1;  // tsegl[lo] <= i < tsegl[hi + 1]
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (tsegl[mid] <= i) lo = mid;
+      else hi = mid - 1;
+    }
+    const int q = (int)i - tsegl[lo];
+    const int n = segl[lo + 1] - segl[lo];
+    tile_info[i] = int4{lo, segl[lo] + q * bm, min(bm, n - q * bm), 0};
+  }
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t ch = (int64_t)blockIdx.x * (SORT_THREADS / 64) + w;
   if (ch >= nch) return;  // whole wave; no block-wide barrier below
