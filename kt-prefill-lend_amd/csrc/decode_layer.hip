@@ -369,15 +369,24 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_gate_up(const __bf16* __re
     }
   };
   load_x(0, min(mch, nm));
+  // the weight loads after the x pieces, every one issued (a lane past the row's units
+  // re-reads its last unit), so that exactly NW vector memory instructions follow the x
+  // pieces: x is quantised while the weights are still on their way
+  __builtin_amdgcn_sched_barrier(0);
   typename U::W w[2][UPL];
 #pragma unroll
-  for (int j = 0; j < UPL; ++j)
-    if (j0 + LPR * j < units) {
-      U::load(wg, j0 + LPR * j, grid, w[0][j]);
-      U::load(wu, j0 + LPR * j, grid, w[1][j]);
-    }
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the x pieces (and the weights) have landed
-  __syncthreads();
+  for (int j = 0; j < UPL; ++j) {
+    const int uj = min(j0 + LPR * j, units - 1);
+    U::load(wg, uj, grid, w[0][j]);
+    U::load(wu, uj, grid, w[1][j]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  constexpr int NW = 2 * UPL * U::NLD;
+  constexpr int NWC = NW < 63 ? NW : 63;
+  __builtin_amdgcn_s_waitcnt((NWC & 15) | ((NWC >> 4) << 14) | (7 << 4) | (15 << 8));  // vmcnt(NWC): x has landed
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_s_barrier();  // every wave's x pieces (no workgroup fence: it would wait for the weights)
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   quantize_x(min(mch, nm));
 #pragma unroll
   for (int j = 0; j < UPL; ++j)

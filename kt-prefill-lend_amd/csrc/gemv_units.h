@@ -73,6 +73,7 @@ struct Unit;
 template <>
 struct Unit<GGML_Q8_0> {
   static constexpr int VALS = 32, NQ = 1;
+  static constexpr int NLD = 3;  // VMEM instructions of load(), at least (a waitcnt counts on it)
   struct W { uint32_t r[9]; uint32_t sh; uint32_t q[8]; float d; };
   __device__ static void load(const uint8_t* row, int u, const uint32_t*, W& w) {
     const uint8_t* b = row + (int64_t)u * QB8_0;
@@ -100,6 +101,7 @@ struct Unit<GGML_Q8_0> {
 template <>
 struct Unit<GGML_Q4_K> {
   static constexpr int VALS = 64, NQ = 2;
+  static constexpr int NLD = 3;  // VMEM instructions of load(), at least (a waitcnt counts on it)
   struct W { u32x4_t h0; uint32_t q[8]; int g; float d, dmin; int sc0, m0, sc1, m1; };
   __device__ static void load(const uint8_t* row, int u, const uint32_t*, W& w) {
     const uint8_t* b = row + (int64_t)(u >> 2) * QB4_K;
@@ -165,6 +167,7 @@ struct Unit<GGML_Q4_K> {
 template <>
 struct Unit<GGML_Q6_K> {
   static constexpr int VALS = 64, NQ = 2;
+  static constexpr int NLD = 8;  // VMEM instructions of load(), at least (a waitcnt counts on it)
   struct W {
     uint32_t rl[9], rh[9], rs[2], rd;
     uint32_t shq, shs, shd;
@@ -237,6 +240,7 @@ struct Unit<GGML_Q6_K> {
 template <>
 struct Unit<GGML_IQ3_S> {
   static constexpr int VALS = 32, NQ = 1;
+  static constexpr int NLD = 5;  // VMEM instructions of load(), at least: the compiler merges q2 and rq[2]
   struct W {
     uint32_t rq[3], rg[2], rd, rh, rsc;
     uint32_t shq, shg, shd, shh, shsc;
