@@ -210,7 +210,9 @@ struct BPiece<GGML_Q6_K> {
 
 template <>
 struct BPiece<GGML_IQ3_S> {
-  static constexpr int NLOAD = 4;  // VMEM instructions per load<SUB>, at least
+  // VMEM instructions per load<SUB>: qs (dwordx2 + dword, merged into one dwordx3), the
+  // signs (dwordx2) and the qh dword
+  static constexpr int NLOAD = 3;
   static constexpr int VPM = 7;    // VALU instructions the GEMM schedule places after each MFMA
   // d and the 4 scale bytes of the block (dwords below them, realigned at decode)
   struct Head { uint32_t dw, sc0, sc1; uint32_t s; };

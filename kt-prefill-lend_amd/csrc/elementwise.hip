@@ -1,46 +1,73 @@
-// Memory-bound kernels of the hot-expert path: GGUF dequantisation to bf16, the hot
+// Memory-bound kernels of the hot-expert path: GGUF dequantisation to bf16 (through the
+// grouped GEMMs' decoder), the hot
 // cache's route lookup, q8_1 activation quantisation, SiLU*mul and the weighted top-k
 // combine.
-#include "formats.h"
+#include "bpiece.h"
 #include "kernels.h"
 
 namespace ktmi {
 
 // ---------------------------------------------------------------- dequant
-// One thread decodes 16 consecutive values and writes them as two 16-byte stores.
-// grid (ceil(rows*cols/16/256), n). P:11471-11498 contract, all four formats.
+// The grouped GEMMs' own decoder (bpiece.h) run stand-alone, so the bytes-to-bf16 step the
+// GEMMs feed to the matrix cores is the one this entry point exposes (and its tests pin):
+// the same lane -> (row, half) map (lane % 32 = row of a 32-row group, lane / 32 = half h
+// of a 64-value step), the same load_head / load<SUB> / decode<SUB> calls. Each wave runs
+// 32 rows over the 4 steps of one 256-value super-block column and writes every decoded
+// 8-value chunk (16 bytes) to its K position 256 sb + ksub<SUB>() + coff(q).
+// grid (ceil(row groups x columns / 4), n); P:11471-11498 contract, all four formats.
+template <int TYPE, int SUB>
+__device__ __forceinline__ void dequant_step(const uint8_t* row, int sb, int h, int64_t cols,
+                                             const typename BPiece<TYPE>::Head& hd, const uint32_t* grid,
+                                             uint16_t* orow) {
+  using BP = BPiece<TYPE>;
+  const int64_t k0 = 256 * (int64_t)sb + BP::template ksub<SUB>();
+  // Q8_0 rows may end inside a super-block column (a piece is one 32-value block): the
+  // pieces past the row's end are not loaded
+  if (k0 + BP::off0(h) >= cols) return;
+  typename BP::Raw raw;
+  uint32_t v[16];
+  BP::template load<SUB>(row, sb, h, grid, raw);
+  BP::template decode<SUB>(hd, raw, grid, v);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int pos = (c < 2 ? BP::off0(h) : BP::off1(h)) + 8 * (c & 1);  // step position of chunk c
+    const u32x4_t w = {v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]};
+    *(u32x4_t*)(orow + k0 + BP::coff(pos / 8)) = w;
+  }
+}
+
 template <int TYPE>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ raw, int64_t raw_stride,
                                                       int64_t rows, int64_t cols, int64_t rb,
                                                       uint16_t* __restrict__ out, int64_t out_stride) {
+  using BP = BPiece<TYPE>;
   __shared__ uint32_t grid[TYPE == GGML_IQ3_S ? 512 : 1];
   if constexpr (TYPE == GGML_IQ3_S) {
     stage_iq3s_grid(grid);
     __syncthreads();
   }
   const int64_t e = blockIdx.y;
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t groups_per_row = cols / 16;
-  if (i >= rows * groups_per_row) return;
-  const int64_t r = i / groups_per_row;
-  const int c0 = (int)(i % groups_per_row) * 16;
-  float y[16];
-  decode16<TYPE>(raw + e * raw_stride + r * rb, c0, grid, y);
-  u32x4_t a, b;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    a[k] = f2bf2(y[2 * k], y[2 * k + 1]);
-    b[k] = f2bf2(y[8 + 2 * k], y[8 + 2 * k + 1]);
-  }
-  u32x4_t* dst = (u32x4_t*)(out + e * out_stride + r * cols + c0);
-  dst[0] = a;
-  dst[1] = b;
+  const int lane = threadIdx.x & 63, h = lane >> 5;
+  const int64_t nsb = (cols + 255) / 256;
+  const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (row group, column)
+  if (unit >= (rows + 31) / 32 * nsb) return;
+  const int64_t r = unit / nsb * 32 + (lane & 31);
+  const int sb = (int)(unit % nsb);
+  if (r >= rows) return;
+  const uint8_t* row = raw + e * raw_stride + r * rb;
+  uint16_t* orow = out + e * out_stride + r * cols;
+  typename BP::Head hd;
+  BP::load_head(row, sb, h, hd);
+  dequant_step<TYPE, 0>(row, sb, h, cols, hd, grid, orow);
+  dequant_step<TYPE, 1>(row, sb, h, cols, hd, grid, orow);
+  dequant_step<TYPE, 2>(row, sb, h, cols, hd, grid, orow);
+  dequant_step<TYPE, 3>(row, sb, h, cols, hd, grid, orow);
 }
 
 int launch_dequant(const uint8_t* raw, int64_t raw_stride, int type, int64_t n, int64_t rows, int64_t cols,
                    uint16_t* out, int64_t out_stride, hipStream_t stream) {
-  const int64_t groups = rows * (cols / 16);
-  dim3 grid((unsigned)((groups + 255) / 256), (unsigned)n);
+  const int64_t units = (rows + 31) / 32 * ((cols + 255) / 256);
+  dim3 grid((unsigned)((units + 3) / 4), (unsigned)n);
   const int64_t rb = row_bytes(cols, type);
   switch (type) {
     case GGML_Q8_0: dequant_kernel<GGML_Q8_0><<<grid, 256, 0, stream>>>(raw, raw_stride, rows, cols, rb, out, out_stride); break;

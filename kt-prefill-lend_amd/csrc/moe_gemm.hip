@@ -52,7 +52,7 @@ constexpr int tile_m() { return WM * FJ * 32; }  // routes per tile
 // activation buffers: steps k .. k+AD-1 in flight (direct global->LDS loads AD-1 steps
 // ahead); rows of 128 B, 16-byte slots swizzled (lds_slot)
 constexpr int AD = 4;
-static_assert(AD * tile_m<8>() * A_ROW + 2048 <= 160 * 1024, "LDS");
+static_assert(AD * tile_m<8>() * A_ROW + 2048 <= 160 * 1024, "LDS: activation buffers + IQ3_S codebook");
 
 // ---- route sort by slot. hist is slot-major: hist[e * nch + chunk].
 
@@ -258,8 +258,12 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes,
   constexpr int A_BYTES = BM * A_ROW;
   constexpr int AJ = A_BYTES / (16 * NTHREADS);  // direct loads per thread per step
   static_assert(AJ % 2 == 0, "A loads are spread over the 2 regions of a step");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[AD * A_BYTES];
-  __shared__ uint32_t grid_lds[TYPE == GGML_IQ3_S ? 512 : 1];
+  // one LDS object: the IQ3_S codebook sits behind the activation buffers. With a second
+  // __shared__ variable the compiler tracks the direct buffer->LDS loads per object and
+  // waits for all of them (vmcnt(0)) before every LDS read, which drains the prefetch.
+  constexpr int GRID_BYTES = TYPE == GGML_IQ3_S ? 512 * 4 : 0;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[AD * A_BYTES + GRID_BYTES];
+  uint32_t* const grid_lds = (uint32_t*)(smem + AD * A_BYTES);
   using BP = BPiece<TYPE>;
 
   // XCD-aware order: workgroups are dealt to the 8 XCDs round-robin (pid % 8). All NT
@@ -357,19 +361,26 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes,
   using S2 = std::integral_constant<int, 2>;
   using S3 = std::integral_constant<int, 3>;
 
-  // prologue: raw(0), raw(1), A(0), A(1), A(2); then wait for A(0) only (the newest
-  // 2 AJ loads stay in flight), which also covers the raw bytes, and decode step 0
+  // prologue in the steady state's issue order (step j issues A(j+3), then raw(j+2)):
+  // A(0), A(1), raw(0), A(2), raw(1), so that at the end of step 0 as many loads follow
+  // A(1) as at any later step; then wait for A(0) only and decode step 0 (its raw bytes
+  // come after A(1): the compiler's wait for them also covers A(1))
+  // (sched_barrier keeps the compiler from hoisting the register loads above the direct ones)
 #pragma unroll
   for (int i = 0; i < FI; ++i) BP::load_head(b_row[i], 0, h, head[i]);
-#pragma unroll
-  for (int i = 0; i < FI; ++i) BP::template load<0>(b_row[i], 0, h, grid_lds, raw[0][i]);
-#pragma unroll
-  for (int i = 0; i < FI; ++i) BP::template load<1>(b_row[i], 0, h, grid_lds, raw[1][i]);
   issue_a(0, S0{}, 0, 0, AJ);
   issue_a(0, S1{}, 1, 0, AJ);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < FI; ++i) BP::template load<0>(b_row[i], 0, h, grid_lds, raw[0][i]);
+  __builtin_amdgcn_sched_barrier(0);
   issue_a(0, S2{}, 2, 0, AJ);
-  static_assert(2 * AJ < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt(wait_vmcnt(2 * AJ));
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < FI; ++i) BP::template load<1>(b_row[i], 0, h, grid_lds, raw[1][i]);
+  __builtin_amdgcn_sched_barrier(0);
+  static_assert(2 * AJ + 2 * FI * BP::NLOAD < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(wait_vmcnt(2 * AJ + 2 * FI * BP::NLOAD));
   __syncthreads();  // A(0) of every wave; the codebook
 #pragma unroll
   for (int i = 0; i < FI; ++i) BP::template decode<0>(head[i], raw[0][i], grid_lds, wv[0][i]);
@@ -443,8 +454,9 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes,
       __builtin_amdgcn_sched_barrier(0);
     }
     // A(k+1) has landed once at most the VMEM ops issued after it are outstanding: A(k+2),
-    // A(k+3) and the raw bytes of steps k+1 and k+2 (at least NLOAD instructions a piece;
-    // the compiler waits for those register loads itself before their decode)
+    // A(k+3) and the raw bytes of steps k+1 and k+2 (NLOAD instructions a piece, the count
+    // the compiler emits; the compiler waits for those register loads itself before their
+    // decode). tests/test_asm_waitcnt.py checks this count against the gfx950 assembly.
     constexpr int NYOUNG = 2 * (AJ + FI * BP::NLOAD);
     static_assert(NYOUNG < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt(wait_vmcnt(NYOUNG));

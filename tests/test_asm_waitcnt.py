@@ -1,7 +1,18 @@
-"""The decode gate/up kernel waits for its x pieces with a counted `s_waitcnt vmcnt(n)`: n must
-not exceed the number of weight-load instructions the compiler emitted after the x loads
-(Unit::NLD per unit), or the wait would let x be read before it lands. This compiles
-decode_layer.hip for gfx950 and checks every instantiation's count in the assembly."""
+"""Counted `s_waitcnt vmcnt(n)` waits checked against the gfx950 assembly the compiler emits.
+
+A counted wait lets the n youngest vector-memory instructions stay in flight; it is correct
+only if at least n such instructions were issued after the load it waits for. The kernels
+derive n from per-format load counts (BPiece<t>::NLOAD, Unit::NLD); these tests compile the
+sources for gfx950 and count the instructions actually emitted.
+
+* decode_gate_up: the x pieces are waited for with n <= the weight loads issued after them.
+* grouped_gemm (every type, gate/up and down, both route-tile heights): at the end of K step
+  k the activation tile of step k+1, whose direct buffer->LDS loads were issued during step
+  k-2, must have landed, so the step-end wait's n must not exceed the vector-memory
+  instructions issued after that tile's last direct load (cyclically over the 4 steps of the
+  unrolled super-block loop, and from the prologue into the first step); the prologue's own
+  wait for tile 0 likewise; and no vmcnt(0) may drain the prefetch inside the K loop.
+"""
 import os
 import re
 import shutil
@@ -14,14 +25,26 @@ ROOT = Path(__file__).resolve().parents[1]
 CSRC = ROOT / "kt-prefill-lend_amd" / "csrc"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
+pytestmark = pytest.mark.skipif(not shutil.which(HIPCC) and not Path(HIPCC).exists(), reason="hipcc not available")
 
-@pytest.mark.skipif(not shutil.which(HIPCC) and not Path(HIPCC).exists(), reason="hipcc not available")
-def test_decode_gate_up_counted_wait_covers_the_weight_loads(tmp_path):
-    out = tmp_path / "decode_layer.s"
+VMEM = re.compile(r"^\s*(global_load|buffer_load)")
+DMA = re.compile(r"^\s*buffer_load\w*\s.*\blds\b")
+
+
+def _asm(src: str, tmp_path) -> list:
+    out = tmp_path / (Path(src).stem + ".s")
     cmd = [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
-           "-packed-fp32-ops", "--cuda-device-only", "-S", str(CSRC / "decode_layer.hip"), f"-I{CSRC}", "-o", str(out)]
-    subprocess.run(cmd, check=True, capture_output=True, timeout=600)
-    lines = out.read_text().split("\n")
+           "-packed-fp32-ops", "--cuda-device-only", "-S", str(CSRC / src), f"-I{CSRC}", "-o", str(out)]
+    subprocess.run(cmd, check=True, capture_output=True, timeout=900)
+    return out.read_text().split("\n")
+
+
+def _vmcnt(line: str) -> int:
+    return int(re.search(r"vmcnt\((\d+)\)", line).group(1))
+
+
+def test_decode_gate_up_counted_wait_covers_the_weight_loads(tmp_path):
+    lines = _asm("decode_layer.hip", tmp_path)
     starts = [i for i, l in enumerate(lines) if re.match(r"^_ZN4ktmi12_GLOBAL__N_114decode_gate_up\w*:", l)]
     assert len(starts) >= 16
     for st in starts:
@@ -29,7 +52,64 @@ def test_decode_gate_up_counted_wait_covers_the_weight_loads(tmp_path):
         marks = [i for i in range(st, end) if "sched_barrier mask(0x00000000)" in lines[i]]
         assert len(marks) >= 2, lines[st]
         a, b = marks[0], marks[1]  # the weight loads sit between the first two
-        loads = sum(1 for i in range(a, b) if re.search(r"\b(global_load|buffer_load)", lines[i]))
+        loads = sum(1 for i in range(a, b) if VMEM.match(lines[i]))
         wait = next(lines[i] for i in range(b, end) if "s_waitcnt" in lines[i])
-        n = int(re.search(r"vmcnt\((\d+)\)", wait).group(1))
+        n = _vmcnt(wait)
         assert 0 < n <= loads, (lines[st].split(":")[0], n, loads)
+
+
+def _k_loop(lines, st, end):
+    labels = {}
+    for i in range(st, end):
+        m = re.match(r"^(\.LBB\w+):", lines[i])
+        if m:
+            labels[m.group(1)] = i
+    loops = []
+    for i in range(st, end):
+        m = re.search(r"s_cbranch_\w+\s+(\.LBB\w+)", lines[i])
+        if m and m.group(1) in labels and labels[m.group(1)] < i:
+            loops.append((labels[m.group(1)], i))
+    # the super-block loop is the one holding the MFMAs
+    return max(loops, key=lambda ab: sum("v_mfma" in lines[j] for j in range(ab[0], ab[1])))
+
+
+def test_grouped_gemm_counted_waits_cover_the_activation_tiles(tmp_path):
+    lines = _asm("moe_gemm.hip", tmp_path)
+    starts = [i for i, l in enumerate(lines) if re.match(r"^_ZN4ktmi12_GLOBAL__N_112grouped_gemm\w*:", l)]
+    assert len(starts) == 16  # 4 types x (gate/up, down) x (256-, 128-route tiles)
+    for st in starts:
+        name = lines[st].split(":")[0]
+        end = next(i for i in range(st + 1, len(lines)) if "s_endpgm" in lines[i])
+        a, b = _k_loop(lines, st, end)
+        body = lines[a:b]
+        assert not [l for l in body if re.search(r"s_waitcnt.*vmcnt\(0\)", l)], (name, "vmcnt(0) in the K loop")
+        bars = [j for j, l in enumerate(body) if l.strip() == "s_barrier"]
+        assert len(bars) == 4, (name, "4 K steps per super-block", len(bars))
+        steps, prev = [], bars[-1] - len(body)
+        for s in range(4):  # step s: the instructions after the previous step's barrier up to its own
+            steps.append([j % len(body) for j in range(prev + 1, bars[s])])
+            prev = bars[s]
+        waits = []
+        for s in range(4):
+            w = next(body[j] for j in reversed(steps[s]) if "s_waitcnt" in body[j] and "vmcnt" in body[j])
+            waits.append(_vmcnt(w))
+            k2 = steps[(s - 2) % 4]
+            dmas = [p for p, j in enumerate(k2) if DMA.match(body[j])]
+            assert dmas, (name, "no direct loads in step", (s - 2) % 4)
+            after = sum(1 for j in k2[dmas[-1] + 1:] if VMEM.match(body[j]))
+            after += sum(1 for j in steps[(s - 1) % 4] if VMEM.match(body[j]))
+            after += sum(1 for j in steps[s] if VMEM.match(body[j]))
+            assert 0 < waits[s] <= after, (name, "step", s, waits[s], after)
+        # the prologue: 3 tiles of AJ direct loads, then the wait for tile 0 and a barrier
+        pro = lines[st:a]
+        dmas = [j for j, l in enumerate(pro) if DMA.match(l)]
+        assert len(dmas) % 3 == 0 and dmas, (name, len(dmas))
+        aj = len(dmas) // 3
+        bar0 = next(j for j in range(dmas[-1], len(pro)) if pro[j].strip() == "s_barrier")
+        w0 = next(pro[j] for j in reversed(range(dmas[-1], bar0)) if "s_waitcnt" in pro[j] and "vmcnt" in pro[j])
+        after0 = sum(1 for l in pro[dmas[aj - 1] + 1:bar0] if VMEM.match(l))
+        assert 0 < _vmcnt(w0) <= after0, (name, "prologue", _vmcnt(w0), after0)
+        # entry into step 0: tile 1 = the prologue's direct loads aj .. 2 aj - 1
+        after1 = sum(1 for l in pro[dmas[2 * aj - 1] + 1:] if VMEM.match(l))
+        after1 += sum(1 for j in steps[0] if j >= 0 and VMEM.match(body[j]) and j < bars[0])
+        assert waits[0] <= after1, (name, "entry", waits[0], after1)

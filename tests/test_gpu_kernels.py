@@ -24,21 +24,25 @@ def test_dequant_bit_exact(dev, t):
 
     DQ, *_ = _pkg()
     rng = np.random.default_rng(100 + t)
-    n, rows, cols = 3, 48, 768 if t == R.GGML_Q8_0 else 512
-    rb = R.row_bytes(cols, t)
-    stride = rows * rb + 64  # padded expert stride
-    raw = np.zeros((n, stride), np.uint8)
-    for e in range(n):
-        raw[e, :rows * rb] = random_blocks(t, rows, cols, rng).reshape(-1)
-    out = torch.full((n, rows * cols + 256), -1, dtype=torch.int16, device=dev).view(torch.bfloat16)
-    view = out[:, :rows * cols].view(n, rows, cols)
-    DQ.dequant_experts(to_dev(raw, dev), stride, t, n, rows, cols, view)
-    torch.cuda.synchronize()
-    got = bf16_bits_of(out)
-    for e in range(n):
-        exp = R.dequant_experts(raw[e, :rows * rb], t, 1, rows, cols).reshape(-1)
-        assert np.array_equal(got[e, :rows * cols], exp), f"type {t} expert {e}"
-        assert np.all(got[e, rows * cols:] == 0xFFFF), "wrote past the expert"
+    # the stand-alone dequant runs the grouped GEMMs' operand decoder (BPiece<t>): 32-row
+    # groups x 256-value columns; the second shape has a partial row group and (Q8_0) a row
+    # that ends halfway through a 64-value step
+    shapes = [(48, 768 if t == R.GGML_Q8_0 else 512), (33, 288 if t == R.GGML_Q8_0 else 256)]
+    for n, (rows, cols) in zip((3, 2), shapes):
+        rb = R.row_bytes(cols, t)
+        stride = (rows * rb + 64 + 15) // 16 * 16  # padded expert stride
+        raw = np.zeros((n, stride), np.uint8)
+        for e in range(n):
+            raw[e, :rows * rb] = random_blocks(t, rows, cols, rng).reshape(-1)
+        out = torch.full((n, rows * cols + 256), -1, dtype=torch.int16, device=dev).view(torch.bfloat16)
+        view = out[:, :rows * cols].view(n, rows, cols)
+        DQ.dequant_experts(to_dev(raw, dev), stride, t, n, rows, cols, view)
+        torch.cuda.synchronize()
+        got = bf16_bits_of(out)
+        for e in range(n):
+            exp = R.dequant_experts(raw[e, :rows * rb], t, 1, rows, cols).reshape(-1)
+            assert np.array_equal(got[e, :rows * cols], exp), f"type {t} expert {e} rows {rows} cols {cols}"
+            assert np.all(got[e, rows * cols:] == 0xFFFF), "wrote past the expert"
 
 
 def test_quantize_q8_1_matches_reference_quantizer(dev):
