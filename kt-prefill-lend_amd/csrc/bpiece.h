@@ -186,22 +186,26 @@ struct BPiece<GGML_Q6_K> {
     const uint32_t sa = alignbyte(hd.w[2 * hh + 1], hd.w[2 * hh], s);
     const uint32_t sbw = alignbyte(hd.w[2 * hh + 2], hd.w[2 * hh + 1], s);
     const float d = half_bits_to_float(alignbyte(hd.w[4], hd.w[4], s) & 0xFFFF);
-    const float d1a = d * (float)(int8_t)((sa >> (16 * c + h8)) & 0xFF);
-    const float d1b = d * (float)(int8_t)((sbw >> (16 * c + h8)) & 0xFF);
+    // y = (d sc) (q - 32) as the product of (d sc / 4), exact, and the signed byte 4 (q - 32),
+    // converted with one v_cvt_f32_i32 (sdwa, sign-extended byte): one rounding of the exact
+    // product, and the signed zeros of a plain multiply (q = 32 under a negative scale
+    // gives -0, as (d sc) * 0 does). The 6-bit code q - 32 is q with its bit 5 flipped, read
+    // as 6-bit two's complement: flipping bits 1, 3, 5, 7 of every qh byte flips bit 5 of
+    // both runs' codes; the code then sits in bits 2..7 of its byte.
+    const float d1a = 0.25f * (d * (float)(int8_t)((sa >> (16 * c + h8)) & 0xFF));
+    const float d1b = 0.25f * (d * (float)(int8_t)((sbw >> (16 * c + h8)) & 0xFF));
     constexpr int hsh = 2 * c;
-    // d1 (q - 32) as fma(d1, q, -32 d1): d1 q - 32 d1 is the exact product, rounded once as
-    // the product itself would be (the bytes convert with one v_cvt_f32_ubyteN each)
-    const float n1a = -32.0f * d1a, n1b = -32.0f * d1b;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t lw = alignbyte(r.ql[i + 1], r.ql[i], s);
-      const uint32_t hw = alignbyte(r.qh[i + 1], r.qh[i], s);
-      const uint32_t va = (lw & 0x0F0F0F0Fu) | (((hw >> hsh) & 0x03030303u) << 4);
-      const uint32_t vb = ((lw >> 4) & 0x0F0F0F0Fu) | (((hw >> (hsh + 4)) & 0x03030303u) << 4);
-      out[2 * i] = f2bf2(__builtin_fmaf(d1a, (float)(va & 0xFF), n1a), __builtin_fmaf(d1a, (float)((va >> 8) & 0xFF), n1a));
-      out[2 * i + 1] = f2bf2(__builtin_fmaf(d1a, (float)((va >> 16) & 0xFF), n1a), __builtin_fmaf(d1a, (float)(va >> 24), n1a));
-      out[8 + 2 * i] = f2bf2(__builtin_fmaf(d1b, (float)(vb & 0xFF), n1b), __builtin_fmaf(d1b, (float)((vb >> 8) & 0xFF), n1b));
-      out[8 + 2 * i + 1] = f2bf2(__builtin_fmaf(d1b, (float)((vb >> 16) & 0xFF), n1b), __builtin_fmaf(d1b, (float)(vb >> 24), n1b));
+      const uint32_t hw = alignbyte(r.qh[i + 1], r.qh[i], s) ^ 0xAAAAAAAAu;
+      // run c: low nibbles and qh bits hsh, hsh+1; run c+2: high nibbles and bits hsh+4, hsh+5
+      const uint32_t va = bfi(0xC0C0C0C0u, hw << (6 - hsh), (lw & 0x0F0F0F0Fu) << 2);
+      const uint32_t vb = bfi(0xC0C0C0C0u, hsh == 2 ? hw : hw << 2, (lw >> 2) & 0x3C3C3C3Cu);
+      out[2 * i] = f2bf2(d1a * (float)(int8_t)(va & 0xFF), d1a * (float)(int8_t)((va >> 8) & 0xFF));
+      out[2 * i + 1] = f2bf2(d1a * (float)(int8_t)((va >> 16) & 0xFF), d1a * (float)(int8_t)(va >> 24));
+      out[8 + 2 * i] = f2bf2(d1b * (float)(int8_t)(vb & 0xFF), d1b * (float)(int8_t)((vb >> 8) & 0xFF));
+      out[8 + 2 * i + 1] = f2bf2(d1b * (float)(int8_t)((vb >> 16) & 0xFF), d1b * (float)(int8_t)(vb >> 24));
     }
   }
   __device__ static int off0(int h) { return 16 * h; }

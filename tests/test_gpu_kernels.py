@@ -3,7 +3,7 @@ import numpy as np
 import pytest
 
 from conftest import bf16_bits_of, bf16_tensor, to_dev
-from helpers import TYPES, random_blocks
+from helpers import _F16_FIELDS, TYPES, random_blocks
 from oracle import gguf_ref as R
 
 pytestmark = pytest.mark.gpu
@@ -16,6 +16,18 @@ def _pkg():
     import kt_prefill_lend_amd.kt_hot_cache as C
 
     return DQ, M, H, C
+
+
+def zero_scales(blocks: np.ndarray, t: int, rng) -> None:
+    """Every third block's fp16 fields become +0 or -0 and (Q6_K) some sub-block scales 0:
+    the dequantised zeros must carry the signs of the oracle's plain products."""
+    blck, ts = R.BLOCK_INFO[t]
+    v = blocks.reshape(blocks.shape[0], -1, ts)
+    for off in _F16_FIELDS[t]:
+        v[:, ::3, off] = 0
+        v[:, ::3, off + 1] = np.where(rng.random(v[:, ::3, off + 1].shape) < 0.5, 0x80, 0).astype(np.uint8)
+    if t == R.GGML_Q6_K:
+        v[:, 1::3, 192:200] = 0
 
 
 @pytest.mark.parametrize("t", TYPES)
@@ -33,7 +45,10 @@ def test_dequant_bit_exact(dev, t):
         stride = (rows * rb + 64 + 15) // 16 * 16  # padded expert stride
         raw = np.zeros((n, stride), np.uint8)
         for e in range(n):
-            raw[e, :rows * rb] = random_blocks(t, rows, cols, rng).reshape(-1)
+            blocks = random_blocks(t, rows, cols, rng)
+            if rows == 33:
+                zero_scales(blocks, t, rng)
+            raw[e, :rows * rb] = blocks.reshape(-1)
         out = torch.full((n, rows * cols + 256), -1, dtype=torch.int16, device=dev).view(torch.bfloat16)
         view = out[:, :rows * cols].view(n, rows, cols)
         DQ.dequant_experts(to_dev(raw, dev), stride, t, n, rows, cols, view)
