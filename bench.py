@@ -400,7 +400,8 @@ def bench_stream(P, torch, S, ev, dev, distinct=2, reps=3):
     tw_d, slot_d = torch.from_numpy(tw).to(dev), torch.from_numpy(slot).to(dev)
     log(f"stream: {nl} layers x {w.hot} experts, {banks[0].gate.nbytes * 2 + banks[0].down.nbytes:,} B per layer pinned,"
         f" prepared in {time.time() - t0:.1f}s")
-    st = SP.KTStreamPrefillGGUF(w.inter, w.hidden, w.top_k, w.types, group_size=w.hot, device=dev)
+    st = SP.KTStreamPrefillGGUF.standalone(w.inter, w.hidden, w.top_k, w.types, group_size=w.hot, device=dev,
+                                           layers=range(nl))
     for i, b in enumerate(banks):
         st.set_bank(i, b)
     stream = L.stream_ptr(dev)

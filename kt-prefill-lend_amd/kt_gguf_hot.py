@@ -29,7 +29,7 @@ from typing import Dict
 import torch
 
 
-from . import _lib
+from . import _lib, sglang_env
 from .gguf import BLOCK_INFO, KERNEL_TYPES, GGUFFile, row_bytes as _row_bytes
 
 try:  # inside SGLang the real combine input type is used
@@ -72,6 +72,11 @@ class GGUFExperts:
 
     def types(self, layer_idx: int):
         return tuple(self.file.ggml_type(f"blk.{layer_idx}.ffn_{p}_exps.weight") for p in ("gate", "up", "down"))
+
+    def layers(self):
+        """The layers that hold routed-expert tensors (blk.{l}.ffn_gate_exps.weight), in order;
+        dense leading layers are skipped."""
+        return [li for li in range(self.num_layers) if self.file.has_tensor(f"blk.{li}.ffn_gate_exps.weight")]
 
     def _view(self, layer_idx: int, proj: str, N: int, rank: int) -> torch.Tensor:
         """This rank's TP part of every expert: rows [N*rank, N*(rank+1)) of gate/up, the
@@ -189,26 +194,43 @@ def silu_and_mul(h: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def _slot_types(layer_idx: int, types) -> tuple:
+    """(type13, type2) of a layer's slots from the GGUF's (gate, up, down) types: the slot
+    rows hold gate and up back to back, so those two must agree, and each type needs a
+    kernel here."""
+    gate, up, down = types
+    if gate != up:
+        raise RuntimeError(f"layer {layer_idx}: the slots keep gate and up rows in one tensor, but the GGUF "
+                           f"stores them as ggml types {gate} and {up}")
+    missing = sorted({t for t in (gate, down) if t not in KERNEL_TYPES})
+    if missing:
+        raise RuntimeError(f"layer {layer_idx}: ggml type(s) {missing} have no kernel in libktmi "
+                           f"(supported: {sorted(KERNEL_TYPES)})")
+    return gate, down
+
+
+def _no_checkpoint_tensors(param, loaded_weight, *args, **kwargs):
+    """weight_loader of the slot tensors: they are filled from the GGUF after loading
+    (process_weights_after_loading), so a checkpoint tensor routed here is a wiring error."""
+    raise RuntimeError("GGUF hot-expert slots are filled from the GGUF file, not from checkpoint tensors")
+
+
 class KTGGUFHotExpertsMethod:
     """GPU-expert method the KT wrapper wraps when the experts are GGUF blocks
-    (hot/kt_gguf_hot.py:163-304)."""
+    (hot/kt_gguf_hot.py:163-304): the same constructor, create_weights /
+    process_weights_after_loading / create_moe_runner / apply signatures and attributes."""
 
     # the streamer's banks cover the hot slots at streamed-prefill sizes (P:10615-10623)
     streams_hot_experts = True
 
     def __init__(self, kt_config, layer):
+        li = kt_config.layer_idx
         self.kt_config = kt_config
         self.num_gpu_experts = kt_config.num_gpu_experts
         self.reader = _reader(kt_config.weight_path)
-        self.rank = getattr(layer, "moe_tp_rank", 0)
-        self.world = getattr(layer, "moe_tp_size", 1)
-        self.types = tuple(self.reader.types(kt_config.layer_idx))
-        if self.types[0] != self.types[1]:
-            raise RuntimeError(f"layer {kt_config.layer_idx}: gate {self.types[0]} and up {self.types[1]} differ")
-        self.type13, self.type2 = self.types[0], self.types[2]
-        for t in (self.type13, self.type2):
-            if t not in KERNEL_TYPES:
-                raise RuntimeError(f"layer {kt_config.layer_idx}: ggml type {t} has no ktmi kernel")
+        self.rank, self.world = getattr(layer, "moe_tp_rank", 0), getattr(layer, "moe_tp_size", 1)
+        self.types = tuple(self.reader.types(li))
+        self.type13, self.type2 = _slot_types(li, self.types)
         self.moe_runner_config = None
         self.mode = _MODES[os.environ.get("KT_HOT_LAYER_MODE", "auto")]
         self._desc = None
@@ -216,41 +238,40 @@ class KTGGUFHotExpertsMethod:
 
     def create_weights(self, layer, num_experts, hidden_size, intermediate_size_per_partition, params_dtype,
                        **extra_weight_attrs):
-        E, N, K = num_experts, intermediate_size_per_partition, hidden_size
-        self.N, self.K = N, K
-        if N * self.world != self.reader.inter or K != self.reader.K:
-            raise RuntimeError(f"GGUF experts {self.reader.inter}x{self.reader.K} vs layer {N}x{self.world} / {K}")
-        if E == 0:
+        """Registers w13_qweight uint8 [E, 2N, rb(K)] and w2_qweight uint8 [E, K, rb(N)]
+        (E = num_experts slots, N = this rank's intermediate rows) on the current device."""
+        self.N, self.K = intermediate_size_per_partition, hidden_size
+        gguf_shape = (self.reader.inter, self.reader.K)
+        if (self.N * self.world, self.K) != gguf_shape:
+            raise RuntimeError(f"the GGUF's experts are {gguf_shape[0]} intermediate x {gguf_shape[1]} hidden; this "
+                               f"layer asks for {self.N} per rank x {self.world} ranks and hidden {self.K}")
+        if num_experts == 0:
             return
         dev = torch.device("cuda", torch.cuda.current_device())
-        w13 = torch.nn.Parameter(torch.empty((E, 2 * N, _row_bytes(K, self.type13)), dtype=torch.uint8, device=dev),
-                                 requires_grad=False)
-        w2 = torch.nn.Parameter(torch.empty((E, K, _row_bytes(N, self.type2)), dtype=torch.uint8, device=dev),
-                                requires_grad=False)
-        w13.weight_loader = w2.weight_loader = self._refuse_loader
-        layer.register_parameter("w13_qweight", w13)
-        layer.register_parameter("w2_qweight", w2)
-
-    @staticmethod
-    def _refuse_loader(param, loaded_weight, *a, **k):
-        raise RuntimeError("GGUF hot experts take no checkpoint expert tensors")
+        shapes = {"w13_qweight": (num_experts, 2 * self.N, _row_bytes(self.K, self.type13)),
+                  "w2_qweight": (num_experts, self.K, _row_bytes(self.N, self.type2))}
+        for name, shape in shapes.items():
+            param = torch.nn.Parameter(torch.empty(shape, dtype=torch.uint8, device=dev), requires_grad=False)
+            param.weight_loader = _no_checkpoint_tensors
+            layer.register_parameter(name, param)
 
     def process_weights_after_loading(self, layer, physical_to_logical=None) -> None:
-        """Fill the slots with this rank's TP slice of logical experts p2l[:E] (identity
-        without a placement map), hot/kt_gguf_hot.py:213-234."""
-        E = self.num_gpu_experts
-        if E == 0:
+        """Copies this rank's TP part of the slots' experts out of the GGUF. Slot s holds
+        logical expert p2l[s]: the map given here, else SGLang's expert-location map for
+        this layer (hot/kt_gguf_hot.py:213-220), else the identity."""
+        n = self.num_gpu_experts
+        if n == 0:
             return
-        p2l = (torch.as_tensor(physical_to_logical[:E], dtype=torch.int64) if physical_to_logical is not None
-               else torch.arange(E))
         li, N = self.kt_config.layer_idx, self.N
-        gate = self.reader.slice(li, "gate", N, self.rank, p2l)
-        up = self.reader.slice(li, "up", N, self.rank, p2l)
-        layer.w13_qweight.data[:, :N].copy_(torch.as_tensor(gate))
-        layer.w13_qweight.data[:, N:].copy_(torch.as_tensor(up))
-        down = torch.as_tensor(self.reader.slice(li, "down", N, self.rank, p2l))
-        assert tuple(down.shape) == tuple(layer.w2_qweight.shape), (down.shape, layer.w2_qweight.shape)
-        layer.w2_qweight.data.copy_(down)
+        p2l = physical_to_logical if physical_to_logical is not None else sglang_env.physical_to_logical(li)
+        experts = torch.arange(n) if p2l is None else torch.as_tensor(p2l, dtype=torch.int64)[:n]
+        w13, w2 = layer.w13_qweight.data, layer.w2_qweight.data
+        for proj, dst in (("gate", w13[:, :N]), ("up", w13[:, N:]), ("down", w2)):
+            src = torch.as_tensor(self.reader.slice(li, proj, N, self.rank, experts))
+            if tuple(src.shape) != tuple(dst.shape):
+                raise RuntimeError(f"layer {li} {proj}: GGUF slice {tuple(src.shape)} does not fit the slots "
+                                   f"{tuple(dst.shape)}")
+            dst.copy_(src)
         self._desc = None
 
     def create_moe_runner(self, layer, moe_runner_config):

@@ -193,14 +193,14 @@ def test_hot_cache_fills_from_banks(tmp_path, monkeypatch):
     plan = cache.plan_swaps(counts)
     assert plan == [(0, 1, 6)]
     for li, s, c in plan:
-        cache._set(li, s, c)
-        cache.fill(li, s, c)
+        cache.assign(li, s, c)
+        cache.load_slot(li, s, c)
     cache.push_tables()
     assert cache.check_tables() == "" and slot_is(0, 1, 6)
     assert abs(cache.gpu_share(counts) - (20 + 50 + 20) / 91) < 1e-9
     # an emptied slot is refilled with the hottest non-resident
-    cache._set(1, 2, C.EMPTY)
+    cache.assign(1, 2, C.EMPTY)
     counts[1, 7] = 9.0
-    assert cache.fill_empty(counts) == 1 and cache.slot2log[1][2] == 7 and slot_is(1, 2, 7)
+    assert cache.fill_empty(counts) == 1 and cache.resident[1][2] == 7 and slot_is(1, 2, 7)
     cache.push_tables()
     assert cache.check_tables() == ""

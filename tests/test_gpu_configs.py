@@ -79,3 +79,112 @@ def test_prefill_chunks(dev, T):
 def test_iq3_s_16k_chunk(dev):
     L, _, _ = _pkg()
     _check(dev, "iq3_s-h2048-n512-e512-k10-hot48", 16384, L.MODE_GROUPED, 64)
+
+
+class _MemExperts:
+    """An expert source over pinned host banks (the streamer's reader interface: E, inter, K,
+    layers(), types(l), banks(l, N, rank, p2l)); bank row e of layer l holds distinct
+    expert (e + l) % D, so every layer routes to a different arrangement."""
+
+    def __init__(self, w, D, layers):
+        import torch
+
+        import kt_prefill_lend_amd.synth as S
+
+        self.E, self.inter, self.K, self.num_layers = w.hot, w.inter, w.hidden, layers
+        self.w = w
+        self.parts = [S.expert_weights(w, s, 0, 16) for s in range(D)]
+        self.D = D
+        N = w.inter
+        self._banks = {}
+        for li in range(layers):
+            rows = [(e + li) % D for e in range(self.E)]
+            gate = torch.from_numpy(np.stack([self.parts[r][0][:N].reshape(-1) for r in rows])).pin_memory()
+            up = torch.from_numpy(np.stack([self.parts[r][0][N:].reshape(-1) for r in rows])).pin_memory()
+            down = torch.from_numpy(np.stack([self.parts[r][1].reshape(-1) for r in rows])).pin_memory()
+            self._banks[li] = [gate, up, down]
+
+    def layers(self):
+        return list(range(self.num_layers))
+
+    def types(self, layer_idx):
+        return self.w.types
+
+    def banks(self, layer_idx, N, rank=0, p2l=None):
+        assert N == self.inter and rank == 0 and p2l is None
+        return self._banks[layer_idx]
+
+
+@pytest.mark.timeout(600)
+def test_streamed_large_expert_layers(dev, monkeypatch):
+    """Large-expert layers (hidden 7168, intermediate 2048, 24 hot Q4_K/Q6_K experts, 6144
+    tokens, 4 layers) through the reference's streamer entry points: stream_prefill_for
+    (method, layer, T) and run(method, layer, dispatch_output, physical_ids), groups of 8
+    experts in the two slots. Each layer against the oracle's FFN on a token sample; the
+    4-layer pipeline (run_layers) equal to the per-layer runs bit for bit; one group of all
+    24 experts equal to the resident layer bit for bit."""
+    from types import SimpleNamespace as NS
+
+    import torch
+
+    import kt_prefill_lend_amd.kt_stream_prefill as SP
+
+    L, H, S = _pkg()
+    w = S.WORKLOADS["q4_k+q6_k-h7168-n2048-e256-k8-hot24-stream4"]
+    T, D, nl = w.tokens[0], 3, w.layers
+    print(f"config 5: quantising {D} experts, pinning {nl} banks", flush=True)
+    src = _MemExperts(w, D, nl)
+    H.register_source("mem://large-experts", src)
+    g, d = dequant_w(np.stack([p[0] for p in src.parts]), np.stack([p[1] for p in src.parts]), w.types, w.hidden,
+                     w.inter)
+    print("config 5: oracle weights ready", flush=True)
+    monkeypatch.setattr(SP, "STREAM_THRESHOLD", 4096)
+    monkeypatch.setattr(SP, "GROUP_SIZE", 8)
+    monkeypatch.setattr(SP, "_instance", None)
+    monkeypatch.setattr(SP, "_failed", False)
+    fl = NS(intermediate_size_per_partition=w.inter, hidden_size=w.hidden, top_k=w.top_k)
+
+    def method(li):
+        kt = NS(layer_idx=li, weight_path="mem://large-experts", num_gpu_experts=w.hot, num_layers=nl)
+        return NS(kt_config=kt, num_gpu_experts=w.hot, gpu_method=NS(streams_hot_experts=True))
+
+    assert SP.stream_prefill_for(method(0), fl, 2048) is None  # below the threshold
+    st = SP.stream_prefill_for(method(0), fl, T)
+    assert st is not None and st.G == 8
+    inputs, outs = [], []
+    sample = np.arange(0, T, 192)
+    for li in range(nl):
+        wl = S.small(w, index=w.index + 100 * li)  # other routing and activations per layer
+        _, tw, slot, _ = S.routing(wl, T)
+        xb = S.activations(wl, T)
+        x, tw_d, ids_d = bf16_tensor(xb, dev), to_dev(tw, dev), to_dev(slot, dev)
+        inputs.append((li, x, tw_d, ids_d))
+        do = H.DispatchOutput(x, H.TopKOutput(tw_d, ids_d, None))
+        y = st.run(method(li), fl, do, ids_d)
+        torch.cuda.synchronize()
+        got = R.bf16_to_f32(bf16_bits_of(y))
+        outs.append(bf16_bits_of(y))
+        mapped = np.where(slot >= 0, (slot + li) % D, -1).astype(np.int32)
+        ref = R.ffn_reference(xb[sample], mapped[sample], tw[sample], g, d)
+        l2, l1, cos = R.rel_errors(got[sample], ref)
+        print(f"config 5 layer {li}: rel L2 {l2:.2e} rel L1 {l1:.2e} cos {cos:.6f}", flush=True)
+        assert l2 < TOL_REL_L2 and cos > 0.999, (li, l2, l1, cos)
+        assert np.all(got[(slot < 0).all(axis=1)] == 0)
+    piped = st.run_layers(inputs)
+    torch.cuda.synchronize()
+    for li, y in enumerate(piped):
+        assert np.array_equal(bf16_bits_of(y), outs[li]), f"pipelined layer {li} differs from its single run"
+    # one group of all 24 experts == the resident layer on the same 24 slots
+    one = SP.KTStreamPrefillGGUF.standalone(w.inter, w.hidden, w.top_k, w.types, group_size=w.hot, device=dev,
+                                            reader=src)
+    li, x, tw_d, ids_d = inputs[0]
+    y1 = bf16_bits_of(one.run_tensors(0, x, tw_d, ids_d))
+    gate, up, down = src._banks[0]
+    W13 = torch.cat([gate.view(w.hot, w.inter, -1), up.view(w.hot, w.inter, -1)], dim=1).to(dev)
+    W2 = down.view(w.hot, w.hidden, -1).to(dev)
+    desc = H.layer_desc(W13, W2, w.hidden, w.inter, w.types[0], w.types[2])
+    yr = bf16_bits_of(H.moe_layer(desc, x, tw_d, ids_d, L.MODE_AUTO))
+    torch.cuda.synchronize()
+    assert np.array_equal(y1, yr), "streamed (one group) and resident layers differ"
+    one.close()
+    st.close()

@@ -89,7 +89,7 @@ def test_gguf_slots_route_and_swaps(dev, tmp_path, monkeypatch):
         torch.cuda.synchronize()
     assert cache.swaps > 0 and cache.check_tables() == ""
     for li in range(L):
-        res = cache.slot2log[li]
+        res = cache.resident[li].tolist()
         assert sum(e >= 10 for e in res) >= 3, res
         for s_, e in enumerate(res):
             assert np.array_equal(layers[li].w13_qweight[s_, N:].cpu().numpy(), raw[(li, "up")][e])
@@ -102,22 +102,38 @@ def test_gguf_slots_route_and_swaps(dev, tmp_path, monkeypatch):
     monkeypatch.setattr(C, "_cache", None)
 
 
-def test_streamer_banks_from_gguf(dev, tmp_path):
+def test_streamer_banks_from_gguf(dev, tmp_path, monkeypatch):
     """A streamed layer over every expert with the banks read from the GGUF (TP rank 1 of
-    2), against the oracle's FFN over the same slices."""
+    2), through the reference's entry points (stream_prefill_for, run with the wrapper's
+    method/layer/dispatch_output), against the oracle's FFN over the same slices."""
     import torch
 
     import kt_prefill_lend_amd.kt_gguf_hot as H
     import kt_prefill_lend_amd.kt_stream_prefill as SP
 
+    from types import SimpleNamespace as NS
+
+    import kt_prefill_lend_amd.sglang_env as SE
+
     p = tmp_path / "tp.gguf"
     make_expert_gguf(p, 1, E, N, K, TYPES, world=2)
-    rd = H.GGUFExperts(str(p))
-    st = SP.KTStreamPrefillGGUF(N, K, TOPK, TYPES, group_size=4, device=dev, reader=rd, rank=1)
+    rd = H._reader(str(p))
+    # the reference wrapper's objects: TP rank 1 of 2, the GPU method streams its hot experts
+    monkeypatch.setattr(SE, "tp_rank_world", lambda: (1, 2))
+    monkeypatch.setattr(SP, "STREAM_THRESHOLD", 32)
+    monkeypatch.setattr(SP, "GROUP_SIZE", 4)
+    monkeypatch.setattr(SP, "_instance", None)
+    monkeypatch.setattr(SP, "_failed", False)
+    kt = NS(layer_idx=0, weight_path=str(p), num_gpu_experts=2, num_layers=1)
+    method = NS(kt_config=kt, num_gpu_experts=2, gpu_method=NS(streams_hot_experts=True))
+    fl = NS(intermediate_size_per_partition=N, hidden_size=K, top_k=TOPK)
     T = 64
+    st = SP.stream_prefill_for(method, fl, T)
+    assert st is not None and st.rank == 1
     ids, tw = _routing(T, 3)
     xb = R.bf16_bits(np.random.default_rng(9).standard_normal((T, K)).astype(np.float32))
-    y = st.run(0, bf16_tensor(xb, dev), to_dev(tw, dev), to_dev(ids, dev))
+    x, ids_d = bf16_tensor(xb, dev), to_dev(ids, dev)
+    y = st.run(method, fl, H.DispatchOutput(x, H.TopKOutput(to_dev(tw, dev), ids_d, None)), ids_d)
     torch.cuda.synchronize()
     got = R.bf16_to_f32(bf16_bits_of(y))
     all_e = list(range(E))

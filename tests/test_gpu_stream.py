@@ -66,12 +66,12 @@ def test_staged_slot_layout(dev):
 
     _, _, SP, _ = _pkg()
     (wl, xb, tw, slot, w13, w2), = _layers(1, 8)
-    st = SP.KTStreamPrefillGGUF(wl.inter, wl.hidden, wl.top_k, wl.types, group_size=4, device=dev)
+    st = SP.KTStreamPrefillGGUF.standalone(wl.inter, wl.hidden, wl.top_k, wl.types, group_size=4, device=dev)
     st.set_bank(0, SP.Bank.from_slot_rows(torch.from_numpy(w13), torch.from_numpy(w2), wl.inter, wl.types))
     for sl, first, n in ((0, 0, 4), (1, 4, 2), (0, 1, 3)):
         st._stage(sl, 0, first, n)
         st.sync_copies()
-        p13, p2 = st.slots[sl]
+        p13, p2 = st.dev.slots[sl]
         got13 = _d2h(p13, n * w13[0].nbytes).reshape(n, *w13.shape[1:])
         got2 = _d2h(p2, n * w2[0].nbytes).reshape(n, *w2.shape[1:])
         assert np.array_equal(got13, w13[first:first + n]), (sl, first, n)
@@ -86,9 +86,9 @@ def test_one_group_equals_resident_layer(dev, T):
 
     _, _, SP, _ = _pkg()
     (wl, xb, tw, slot, w13, w2), = _layers(1, T)
-    st = SP.KTStreamPrefillGGUF(wl.inter, wl.hidden, wl.top_k, wl.types, group_size=wl.hot, device=dev)
+    st = SP.KTStreamPrefillGGUF.standalone(wl.inter, wl.hidden, wl.top_k, wl.types, group_size=wl.hot, device=dev)
     st.set_bank(0, SP.Bank.from_slot_rows(torch.from_numpy(w13), torch.from_numpy(w2), wl.inter, wl.types))
-    y = st.run(0, bf16_tensor(xb, dev), to_dev(tw, dev), to_dev(slot, dev))
+    y = st.run_tensors(0, bf16_tensor(xb, dev), to_dev(tw, dev), to_dev(slot, dev))
     torch.cuda.synchronize()
     got, res = bf16_bits_of(y), _resident(dev, wl, xb, tw, slot, w13, w2)
     g, d = dequant_w(w13, w2, wl.types, wl.hidden, wl.inter)
@@ -111,12 +111,12 @@ def test_groups_and_layers_pipeline(dev):
     _, _, SP, _ = _pkg()
     layers = _layers(3, 40)
     wl0 = layers[0][0]
-    st = SP.KTStreamPrefillGGUF(wl0.inter, wl0.hidden, wl0.top_k, wl0.types, group_size=4, device=dev)
+    st = SP.KTStreamPrefillGGUF.standalone(wl0.inter, wl0.hidden, wl0.top_k, wl0.types, group_size=4, device=dev)
     for i, (wl, xb, tw, slot, w13, w2) in enumerate(layers):
         st.set_bank(i, SP.Bank.from_slot_rows(torch.from_numpy(w13), torch.from_numpy(w2), wl.inter, wl.types))
     singles = []
     for i, (wl, xb, tw, slot, w13, w2) in enumerate(layers):
-        y = st.run(i, bf16_tensor(xb, dev), to_dev(tw, dev), to_dev(slot, dev))
+        y = st.run_tensors(i, bf16_tensor(xb, dev), to_dev(tw, dev), to_dev(slot, dev))
         torch.cuda.synchronize()
         got = bf16_bits_of(y)
         singles.append(got)
@@ -138,7 +138,7 @@ def test_streamer_rejects_bad_groups(dev):
 
     L, _, SP, _ = _pkg()
     (wl, xb, tw, slot, w13, w2), = _layers(1, 8)
-    st = SP.KTStreamPrefillGGUF(wl.inter, wl.hidden, wl.top_k, wl.types, group_size=4, device=dev)
+    st = SP.KTStreamPrefillGGUF.standalone(wl.inter, wl.hidden, wl.top_k, wl.types, group_size=4, device=dev)
     st.set_bank(0, SP.Bank.from_slot_rows(torch.from_numpy(w13), torch.from_numpy(w2), wl.inter, wl.types))
     with pytest.raises(RuntimeError, match="group of at most"):
         st._stage(0, 0, 0, 5)

@@ -125,7 +125,7 @@ def test_hot_cache_host_logic():
     c.seed()
     assert c.check_tables() == ""
     assert c.log2slot_cpu[0, :3].tolist() == [0, 1, 2] and c.log2cpu_cpu[0, :4].tolist() == [-1, -1, -1, 3]
-    c._set(1, 0, 7)
+    c.assign(1, 0, 7)
     c.push_tables()
     assert c.check_tables() == ""
     assert c.log2slot_cpu[1, 7] == 0 and c.log2cpu_cpu[1, 0] == 0
@@ -141,7 +141,44 @@ def test_hot_cache_host_logic():
     assert len(plan) == 1
     # a broken table is reported
     c.log2cpu_cpu[0, 5] = -1
-    assert c.check_tables() != ""
+    assert "neither side" in c.check_tables()
+    with pytest.raises(ValueError, match="another slot"):
+        c.assign(1, 1, 7)  # expert 7 already sits in slot 0 of layer 1
+
+
+def test_swap_pairing_rules():
+    """pair_swaps: coldest slots (empty first) against the hottest non-residents, the
+    margin test per pair, the first failing pair ends the list, ties by index, at most
+    `limit` swaps; brute-forced against an explicit enumeration of the rule."""
+    import kt_prefill_lend_amd.kt_hot_cache as C
+
+    res = np.array([3, C.EMPTY, 0, 5])
+    counts = np.array([4.0, 9.0, 9.0, 1.0, 0.0, 2.0, 7.0, 0.0])
+    # slots by (score, index): slot 1 (empty, -1), slot 3 (expert 5: 2), slot 0 (expert 3: 1)...
+    # scores: slot0=1 (e3), slot1=-1, slot2=4 (e0), slot3=2 (e5) -> order 1, 0, 3, 2
+    # candidates by (-count, id): 1 (9), 2 (9), 6 (7), 4 (0), 7 (0)
+    assert C.pair_swaps(res, counts, 1.5, 8) == [(1, 1), (0, 2), (3, 6)]  # 9 > -1.5, 9 > 1.5, 7 > 3; 0 fails
+    assert C.pair_swaps(res, counts, 1.5, 2) == [(1, 1), (0, 2)]
+    assert C.pair_swaps(res, counts, 5.0, 8) == [(1, 1), (0, 2)]  # 7 > 5*2 fails, ends the list
+    assert C.pair_swaps(res, np.zeros(8), 1.5, 8) == []  # a candidate needs a positive count
+    rng = np.random.default_rng(3)
+    for _ in range(200):
+        E, S = 12, 4
+        res = rng.permutation(E)[:S].astype(np.int64)
+        res[rng.random(S) < 0.2] = C.EMPTY
+        counts = rng.integers(0, 5, E).astype(float)
+        margin = float(rng.choice([1.0, 1.5, 2.0]))
+        got = C.pair_swaps(res, counts, margin, 3)
+        score = [counts[e] if e >= 0 else -1.0 for e in res]
+        slots = sorted(range(S), key=lambda s: (score[s], s))
+        cands = sorted(set(range(E)) - set(int(e) for e in res if e >= 0), key=lambda e: (-counts[e], e))
+        want = []
+        for k in range(min(3, len(cands))):
+            if counts[cands[k]] > 0 and counts[cands[k]] > margin * score[slots[k]]:
+                want.append((slots[k], cands[k]))
+            else:
+                break
+        assert got == want
 
 
 def test_cpu_mask_hook(monkeypatch):
@@ -182,12 +219,151 @@ def test_stream_bank_validation_and_threshold(monkeypatch):
     with pytest.raises(RuntimeError, match="gate/up types"):
         SP.Bank(torch.zeros((3, pg), dtype=torch.uint8), torch.zeros((3, pu), dtype=torch.uint8),
                 torch.zeros((3, pd), dtype=torch.uint8), (12, 14, 14))
+
+
+def _stand_ins(layer_idx=3, streams_hot=True, num_gpu_experts=4, path="/nonexistent.gguf"):
+    """A KT wrapper method and a FusedMoE layer as the reference's wrapper hands them over
+    (only the attributes the streamer and the hot method read)."""
+    from types import SimpleNamespace as NS
+
+    kt = NS(layer_idx=layer_idx, weight_path=path, num_gpu_experts=num_gpu_experts, num_layers=4)
+    method = NS(kt_config=kt, num_gpu_experts=num_gpu_experts, gpu_method=NS(streams_hot_experts=streams_hot))
+    layer = NS(intermediate_size_per_partition=256, hidden_size=512, top_k=8, moe_tp_rank=0, moe_tp_size=1)
+    return method, layer
+
+
+def test_stream_prefill_entry_points(monkeypatch):
+    """stream_prefill_for / stream_prefill_init_early / preallocate with the reference's
+    signatures (P:10515, 10581, 40607, 40995-41024): threshold, capture and failure
+    handling, one process-wide instance built from (method, layer)."""
+    import kt_prefill_lend_amd.kt_stream_prefill as SP
+
+    made = []
+
+    class Fake:
+        def __init__(self, method, layer):
+            made.append((method, layer))
+            self.banks_built, self.rank = False, 0
+
+        def build_all_banks(self):
+            self.banks_built = True
+
+    method, layer = _stand_ins()
+    monkeypatch.setattr(SP, "KTStreamPrefillGGUF", Fake)
+    monkeypatch.setattr(SP, "_instance", None)
+    monkeypatch.setattr(SP, "_failed", False)
     monkeypatch.setattr(SP, "STREAM_THRESHOLD", 0)
-    assert SP.stream_prefill_for(N, K, 8, types, 100000) is None
+    assert SP.stream_prefill_for(method, layer, 100000) is None
+    assert SP.preallocate(layer) is None  # streaming off: nothing is made
+    SP.stream_prefill_init_early(method, layer)
+    assert not made
     monkeypatch.setattr(SP, "STREAM_THRESHOLD", 4096)
-    monkeypatch.setattr(SP, "preallocate", lambda *a, **k: "streamer")
-    assert SP.stream_prefill_for(N, K, 8, types, 1024) is None
-    assert SP.stream_prefill_for(N, K, 8, types, 8192) == "streamer"
+    assert SP.stream_prefill_for(method, layer, 1024) is None and not made
+    st = SP.stream_prefill_for(method, layer, 8192)
+    assert isinstance(st, Fake) and made == [(method, layer)]
+    assert SP.stream_prefill_for(method, layer, 4096) is st and len(made) == 1  # one instance per process
+    # early init: only with KT_GPU_STREAM_EARLY_INIT=1, and it builds every bank
+    monkeypatch.setattr(SP, "_instance", None)
+    monkeypatch.setattr(SP, "EARLY_INIT", False)
+    SP.stream_prefill_init_early(method, layer)
+    assert SP._instance is None
+    monkeypatch.setattr(SP, "EARLY_INIT", True)
+    SP.stream_prefill_init_early(method, layer)
+    assert SP._instance is not None and SP._instance.banks_built
+    # a failed init is remembered: later calls return None instead of retrying
+    monkeypatch.setattr(SP, "_instance", None)
+
+    def broken(method, layer):
+        raise RuntimeError("no GGUF")
+
+    monkeypatch.setattr(SP, "KTStreamPrefillGGUF", broken)
+    with pytest.raises(RuntimeError, match="no GGUF"):
+        SP.stream_prefill_for(method, layer, 8192)
+    assert SP._failed and SP.stream_prefill_for(method, layer, 8192) is None
+
+
+def test_stream_run_takes_the_reference_arguments(monkeypatch):
+    """run(method, layer, dispatch_output, physical_ids): the layer index comes from
+    method.kt_config, x and the route weights from dispatch_output, and the first streamed
+    expert is 0 when the GPU method streams its hot experts, else num_gpu_experts."""
+    import torch
+
+    import kt_prefill_lend_amd.kt_gguf_hot as H
+    import kt_prefill_lend_amd.kt_stream_prefill as SP
+
+    seen = []
+    st = SP.KTStreamPrefillGGUF.__new__(SP.KTStreamPrefillGGUF)
+    st.geometry = SP._Geometry(256, 512, {3: (12, 12, 14)})
+    st._checked = True
+    st.run_tensors = lambda li, x, w, ids, first=0: seen.append((li, x, w, ids, first)) or "acc"
+    x, w, ids = torch.zeros((2, 512)), torch.ones((2, 8)), torch.zeros((2, 8), dtype=torch.int32)
+    d = H.DispatchOutput(x, H.TopKOutput(w, ids, None))
+    for streams_hot, first in ((True, 0), (False, 4)):
+        method, layer = _stand_ins(streams_hot=streams_hot)
+        assert st.run(method, layer, d, ids) == "acc"
+        li, xs, ws, i2, f = seen[-1]
+        assert (li, f) == (3, first) and xs is x and ws is w and i2 is ids
+
+
+def test_sglang_expert_location_map_places_the_slots(monkeypatch):
+    """process_weights_after_loading(layer) reads SGLang's expert-location map for its layer
+    when SGLang is there (hot/kt_gguf_hot.py:213-220): slot s gets logical expert p2l[s];
+    without SGLang or with no metadata the slots hold experts 0..n-1."""
+    import sys
+    import types as T
+
+    import torch
+
+    import kt_prefill_lend_amd.kt_gguf_hot as H
+
+    E, N, K, n, li = 8, 256, 256, 3, 1
+
+    class Source:  # expert e's bytes are all e (gate), e + 64 (up), e + 128 (down)
+        inter, K_, types_ = N, K, (12, 12, 14)
+
+        def types(self, layer_idx):
+            return self.types_
+
+        def slice(self, layer_idx, proj, N_, rank, experts):
+            rows, rb = (N_, H._row_bytes(K, 12)) if proj != "down" else (K, H._row_bytes(N_, 14))
+            base = {"gate": 0, "up": 64, "down": 128}[proj]
+            ex = torch.as_tensor(experts, dtype=torch.int64)
+            return (ex.to(torch.uint8) + base).view(-1, 1, 1).expand(len(ex), rows, rb).contiguous()
+
+    src = Source()
+    src.K = K
+    H.register_source("mem://experts", src)
+    method, layer = _stand_ins(layer_idx=li, num_gpu_experts=n, path="mem://experts")
+    m = H.KTGGUFHotExpertsMethod(method.kt_config, layer)
+    m.N, m.K = N, K
+    mod = torch.nn.Module()
+    mod.register_parameter("w13_qweight", torch.nn.Parameter(torch.zeros((n, 2 * N, H._row_bytes(K, 12)),
+                                                                         dtype=torch.uint8), requires_grad=False))
+    mod.register_parameter("w2_qweight", torch.nn.Parameter(torch.zeros((n, K, H._row_bytes(N, 14)),
+                                                                        dtype=torch.uint8), requires_grad=False))
+
+    def slots():
+        return ([int(mod.w13_qweight[s, 0, 0]) for s in range(n)], [int(mod.w13_qweight[s, N, 0]) - 64 for s in range(n)],
+                [int(mod.w2_qweight[s, 0, 0]) - 128 for s in range(n)])
+
+    for name in ("sglang", "sglang.srt", "sglang.srt.eplb", "sglang.srt.eplb.expert_location_dispatch"):
+        monkeypatch.delitem(sys.modules, name, raising=False)
+    m.process_weights_after_loading(mod)  # no SGLang: identity
+    assert slots() == ([0, 1, 2],) * 3
+    p2l = torch.tensor([[0, 1, 2, 3, 4, 5, 6, 7], [5, 2, 7, 0, 1, 3, 4, 6]])
+    meta = T.SimpleNamespace(physical_to_logical_map_cpu=p2l)
+    fake = T.ModuleType("sglang.srt.eplb.expert_location_dispatch")
+    fake.get_global_expert_location_metadata = lambda: meta
+    for name in ("sglang", "sglang.srt", "sglang.srt.eplb"):
+        monkeypatch.setitem(sys.modules, name, T.ModuleType(name))
+    monkeypatch.setitem(sys.modules, "sglang.srt.eplb.expert_location_dispatch", fake)
+    m.process_weights_after_loading(mod)  # layer 1's map
+    assert slots() == ([5, 2, 7],) * 3
+    fake.get_global_expert_location_metadata = lambda: None
+    m.process_weights_after_loading(mod)  # SGLang without a map: identity
+    assert slots() == ([0, 1, 2],) * 3
+    m.process_weights_after_loading(mod, physical_to_logical=[6, 4, 1])  # an explicit map wins
+    assert slots() == ([6, 4, 1],) * 3
 
 
 def test_layer_argument_errors_before_device_work():
