@@ -132,6 +132,17 @@ int ktmi_moe_layer(const ktmi_layer* layer, const void* x, const float* topk_w, 
 /* The mode KTMI_MODE_AUTO picks for this many routes. */
 int ktmi_moe_layer_mode(const ktmi_layer* layer, int64_t tokens, int64_t top_k);
 
+/* ktmi_moe_layer without a workspace argument. No counterpart in the reference: this is for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). The workspace is a library-owned device array of
+ * KTMI_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; a call whose workspace
+ * (ktmi_moe_layer_workspace) is larger fails with KTMI_ESPACE. It allocates nothing. Every
+ * call on one GPU shares that GPU's array, so calls that overlap on one GPU (two streams or
+ * two threads without ordering between them) race. */
+#define KTMI_NOALLOC_SCRATCH_BYTES (64ll << 20)
+int ktmi_moe_layer_noalloc(const ktmi_layer* layer, const void* x, const float* topk_w, const int32_t* slot_ids,
+                           int64_t tokens, int64_t top_k, void* y, int mode, void* stream);
+
 /* Stage timing for benchmarks (no counterpart in the reference, whose per-layer timers are
  * host-side, P:40981-40985). events: KTMI_STAGE_EVENTS hipEvent_t handles that the next
  * ktmi_moe_layer calls on this thread record on their stream at the stage boundaries:

@@ -16,6 +16,7 @@ KTMI_OK = 0
 KTMI_F32, KTMI_F16, KTMI_BF16 = 0, 1, 2
 MODE_AUTO, MODE_GEMV, MODE_GROUPED = 0, 1, 2
 STAGE_EVENTS = 6
+NOALLOC_SCRATCH_BYTES = 64 << 20  # KTMI_NOALLOC_SCRATCH_BYTES
 
 _i64, _i32, _vp = C.c_int64, C.c_int, C.c_void_p
 
@@ -63,6 +64,7 @@ SIGNATURES = {
     "ktmi_moe_layer_workspace": (_i64, [C.POINTER(ktmi_layer), _i64, _i64, _i32]),
     "ktmi_moe_layer": (_i32, [C.POINTER(ktmi_layer), _vp, _vp, _vp, _i64, _i64, _vp, _vp, _i64, _i32, _vp]),
     "ktmi_moe_layer_mode": (_i32, [C.POINTER(ktmi_layer), _i64, _i64]),
+    "ktmi_moe_layer_noalloc": (_i32, [C.POINTER(ktmi_layer), _vp, _vp, _vp, _i64, _i64, _vp, _i32, _vp]),
     "ktmi_set_stage_events": (_i32, [C.POINTER(C.c_void_p), _i32]),
     "ktmi_quantize_rows_host": (_i32, [_vp, _i64, _i64, _i32, _vp, _i32]),
     "ktmi_streamer_create": (_vp, [_i64, _i64, _i64, _i32]),

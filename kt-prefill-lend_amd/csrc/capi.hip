@@ -1,4 +1,6 @@
 // extern "C" entry points of libktmi.so: argument checks, workspace carve-up, dispatch.
+#include <mutex>
+
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -153,6 +155,33 @@ int ktmi_combine(const void* out, int dtype, const float* w, int64_t T, int64_t 
   return launch_combine(out, dtype, w, T, top_k, K, res, (hipStream_t)stream);
 }
 
+// ---- scratch for ktmi_moe_layer_noalloc
+// A file-scope device array that stands in for the caller's workspace. In host code its
+// name is a host-side stand-in, not a device address: the address on each device comes
+// from hipGetSymbolAddress, taken once per device with that device current, and only that
+// address is ever handed to kernels. Each GPU holds its own copy until the process ends.
+static __device__ __align__(256) uint8_t scratch[KTMI_NOALLOC_SCRATCH_BYTES];
+static constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices] = {};
+
+static int scratch_of_current_device(void** out) {
+  int dev = 0;
+  KTMI_HIP_TRY(hipGetDevice(&dev));
+  KTMI_REQUIRE(dev >= 0 && dev < kMaxDevices, KTMI_EINVAL, "moe_layer_noalloc: device %d (at most %d)", dev,
+               kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    KTMI_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    KTMI_REQUIRE(p != nullptr, KTMI_EHIP, "moe_layer_noalloc: no device address for the scratch array on device %d",
+                 dev);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return KTMI_OK;
+}
+
 int ktmi_moe_layer_mode(const ktmi_layer* L, int64_t tokens, int64_t top_k) {
   (void)L;
   return tokens * top_k <= kGemvMaxRoutes ? KTMI_MODE_GEMV : KTMI_MODE_GROUPED;
@@ -244,6 +273,26 @@ int ktmi_moe_layer(const ktmi_layer* L, const void* x, const float* topk_w, cons
   GroupedPlan P = grouped_plan(tokens, top_k, L->n_slots, K, N);
   return launch_grouped_layer(L, (const uint16_t*)x, topk_w, slot_ids, tokens, top_k, (uint16_t*)y,
                               (uint8_t*)workspace, P, s);
+}
+
+int ktmi_moe_layer_noalloc(const ktmi_layer* L, const void* x, const float* topk_w, const int32_t* slot_ids,
+                           int64_t tokens, int64_t top_k, void* y, int mode, void* stream) {
+  g_err[0] = 0;
+  int rc = check_layer(L);
+  if (rc) return rc;
+  KTMI_REQUIRE(tokens >= 0 && top_k > 0, KTMI_EINVAL, "moe_layer_noalloc: tokens %lld top_k %lld", (long long)tokens,
+               (long long)top_k);
+  if (tokens == 0) return KTMI_OK;
+  if (mode == KTMI_MODE_AUTO) mode = ktmi_moe_layer_mode(L, tokens, top_k);
+  const int64_t need = ktmi_moe_layer_workspace(L, tokens, top_k, mode);
+  KTMI_REQUIRE(need <= KTMI_NOALLOC_SCRATCH_BYTES, KTMI_ESPACE,
+               "moe_layer_noalloc: %lld tokens x top-%lld need %lld bytes of scratch, more than the %lld bytes the "
+               "library holds per GPU (call ktmi_moe_layer with a workspace instead)",
+               (long long)tokens, (long long)top_k, (long long)need, (long long)KTMI_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  rc = scratch_of_current_device(&ws);
+  if (rc) return rc;
+  return ktmi_moe_layer(L, x, topk_w, slot_ids, tokens, top_k, y, ws, KTMI_NOALLOC_SCRATCH_BYTES, mode, stream);
 }
 
 }  // extern "C"
