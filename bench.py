@@ -189,15 +189,18 @@ def main():
     log(f"layer {ms:.3f} ms/step, {tok_s / 1e6:.2f} M tok/s, {layer_tflops:.0f} TFLOP/s "
         f"({100 * layer_tflops / PEAK_BF16_TFLOPS:.1f}% of bf16 peak); stages ms {stages}")
 
-    traffic = None
-    tfile = ROOT / "profiles" / "traffic.json"
-    if tfile.exists():
+    def profiled(fname, field):
+        # a figure of the dominant kernel from a committed rocprofv3 summary (None if absent)
+        f = ROOT / "profiles" / fname
         try:
-            tj = json.loads(tfile.read_text())
-            rec = tj.get(f"{HEADLINE}:T{T}:{dom}")
-            traffic = int(rec["bytes"]) if rec else None
+            rec = json.loads(f.read_text()).get(f"{HEADLINE}:T{T}:{dom}")
+            return rec[field] if rec else None
         except Exception:  # noqa: BLE001
-            traffic = None
+            return None
+
+    traffic = profiled("traffic.json", "bytes")
+    mfma_busy = profiled("mfma.json", "mfma_busy")
+    clock = profiled("mfma.json", "clock_GHz")
 
     result = {
         "metric": "hot-expert MoE layer tokens/s @16K chunk; % of HBM/MFMA roofline",
@@ -217,6 +220,7 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+                     "mfma_busy_counter": mfma_busy, "clock_GHz_counter": clock,
                      "layer_frac": round(layer_tflops / PEAK_BF16_TFLOPS, 4),
                      "stage_ms": {k: round(v, 4) for k, v in stages.items()}},
         "cpu_baseline": None,
@@ -275,40 +279,77 @@ def bench_configs(P, torch, S, ev, dev, steps=10, warmup=2):
     return res
 
 
-def bench_decode(P, torch, S, ev, dev, steps=50, warmup=5):
-    """Decode-shaped layer (Q4_K, 32 hot slots) at 1/4/8/16 tokens: GB/s against HBM with the
-    weights rotated over enough copies to exceed the 256 MB Infinity Cache ("hbm") and with
-    one copy ("warm"). GB/s = algorithmic bytes / step time (both kernels and the gap between
-    them)."""
+def bench_decode(P, torch, S, ev, dev, steps=50, warmup=5, rotate_bytes=512e6):
+    """Decode-shaped layer (Q4_K, 32 hot slots) at 1/4/8/16 tokens: GB/s against HBM.
+    "hbm": the weights rotate over enough copies that the copies' touched bytes exceed
+    `rotate_bytes` (twice the 256 MB Infinity Cache) at every T; "warm": one copy. GB/s =
+    algorithmic bytes / step time (both kernels and the gap between them). "floor": the same
+    byte count read by one plain reduction kernel over rotated buffers, and the time of two
+    back-to-back launches of a one-element kernel (the two-launch layer's fixed cost)."""
     H, L = P.kt_gguf_hot, P._lib
     w = S.WORKLOADS[DECODE]
     w13, w2 = S.slot_tensors(w)
-    per_copy = w13.nbytes + w2.nbytes
-    ncopy = max(8, int(np.ceil(600e6 / per_copy)))
+    from kt_prefill_lend_amd.gguf import row_bytes
+
+    exp_bytes = 2 * w.inter * row_bytes(w.hidden, w.types[0]) + w.hidden * row_bytes(w.inter, w.types[2])
+    cases = []
+    for T in w.tokens:
+        ids, tw, slot, _ = S.routing(w, T)
+        uniq = len(set(slot[slot >= 0].tolist()))
+        cases.append((T, tw, slot, uniq, max(8, int(np.ceil(rotate_bytes / (uniq * exp_bytes))))))
+    ncopy = max(c[4] for c in cases)
     W13 = torch.from_numpy(w13).to(dev)
     W2 = torch.from_numpy(w2).to(dev)
     copies = [(W13.clone(), W2.clone()) for _ in range(ncopy)]
     descs = [H.layer_desc(a, b, w.hidden, w.inter, w.types[0], w.types[2]) for a, b in copies]
+    log(f"decode: {ncopy} copies of the {w.hot} slots ({ncopy * (w13.nbytes + w2.nbytes) / 1e9:.2f} GB)")
     res = {}
-    from kt_prefill_lend_amd.gguf import row_bytes
-
-    exp_bytes = 2 * w.inter * row_bytes(w.hidden, w.types[0]) + w.hidden * row_bytes(w.inter, w.types[2])
-    for T in w.tokens:
-        ids, tw, slot, _ = S.routing(w, T)
+    for T, tw, slot, uniq, nc in cases:
         x = torch.from_numpy(S.activations(w, T).view(np.int16)).to(dev).view(torch.bfloat16)
         tw_d, slot_d = torch.from_numpy(tw).to(dev), torch.from_numpy(slot).to(dev)
-        uniq = len(set(slot[slot >= 0].tolist()))
         nbytes = uniq * exp_bytes + 2 * T * w.hidden * 2
         out = {}
-        for name, dl in (("hbm", descs), ("warm", descs[:1])):
+        for name, dl in (("hbm", descs[:nc]), ("warm", descs[:1])):
             ms, stages, _ = time_layer(P, torch, dl, x, tw_d, slot_d, L.MODE_GEMV, steps, warmup, ev)
             gbs = nbytes / (ms * 1e-3) / 1e9
             out[name] = {"ms_per_step": round(ms, 4), "GBps": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
                          "stage_ms_with_events": {k: round(v, 4) for k, v in stages.items()}}
+        out["hbm"]["copies"], out["hbm"]["rotated_bytes"] = nc, nc * uniq * exp_bytes
+        out["floor"] = decode_floor(torch, ev, dev, uniq * exp_bytes, nc, steps)
         res[f"T{T}"] = {"hot_routes": int((slot >= 0).sum()), "unique_experts": uniq, "bytes": nbytes, **out}
         log(f"decode T={T}: {res[f'T{T}']}")
     del copies
     return res
+
+
+def decode_floor(torch, ev, dev, nbytes, ncopy, steps):
+    """Speed-of-light references for a decode step reading `nbytes` of weights: one plain
+    reduction (torch.amax over int32) of nbytes from buffers rotated over `ncopy` copies, and
+    two back-to-back launches of a one-element fill."""
+    L = load_pkg()._lib
+    stream = L.stream_ptr(dev)
+    n = max(1, int(nbytes) // 4)
+    bufs = [torch.ones(n, dtype=torch.int32, device=dev) for _ in range(ncopy)]
+    tiny = torch.zeros(1, dtype=torch.float32, device=dev)
+    se = ev.create(4)
+
+    def timed(fn, a, b):
+        for i in range(3):
+            fn(i)
+        torch.cuda.synchronize()
+        ev.record(se[a], stream)
+        for i in range(steps):
+            fn(i)
+        ev.record(se[b], stream)
+        torch.cuda.synchronize()
+        return ev.ms(se[a], se[b]) / steps
+
+    read_ms = timed(lambda i: torch.amax(bufs[i % ncopy]), 0, 1)
+    launch_ms = timed(lambda i: (tiny.fill_(i), tiny.fill_(i + 1)), 2, 3)
+    ev.destroy(se)
+    del bufs
+    return {"read_ms": round(read_ms, 4), "read_GBps": round(4 * n / (read_ms * 1e-3) / 1e9, 1),
+            "two_launches_ms": round(launch_ms, 4)}
 
 
 def bench_hybrid(P, torch, S, ev, dev, distinct=16, reps=100, warmup=5):
@@ -376,7 +417,7 @@ def bench_hybrid(P, torch, S, ev, dev, distinct=16, reps=100, warmup=5):
     return res
 
 
-def bench_stream(P, torch, S, ev, dev, distinct=2, reps=3):
+def bench_stream(P, torch, S, ev, dev, distinct=4, reps=3):
     """Large-expert layers streamed from pinned host memory (hidden 7168, intermediate 2048,
     24 hot Q4_K/Q6_K experts per layer, 6144-token chunk, 4 layers): each layer's experts
     are one group; layer l+1's copy overlaps layer l's grouped layer. Weights: `distinct`

@@ -65,7 +65,9 @@ def forward(x_bf16: np.ndarray, slot_ids: np.ndarray, weights: np.ndarray, w13: 
 
 
 def default_threads() -> int:
-    """The host cores this process may use (sched affinity), at most 16."""
+    """The threads the CPU baseline uses: the cores this process may run on (sched affinity),
+    at most 16 (the CPU share a one-GPU box grants a job; a larger pool would only contend
+    with the other jobs on the host)."""
     try:
         n = len(os.sched_getaffinity(0))
     except AttributeError:
@@ -73,28 +75,78 @@ def default_threads() -> int:
     return max(1, min(16, n))
 
 
-def bench(S, w, cpu_tokens: int, T: int, log=print, min_seconds: float = 10.0, max_seconds: float = 30.0):
-    """Times forward() on the first `cpu_tokens` tokens of the T-token chunk of workload `w`
-    (same routing, activations and hot-slot weights as the GPU run), repeating the call
-    until at least `min_seconds` have passed. Returns the cpu_baseline record."""
-    ids, tw, slot, _ = S.routing(w, T)
-    xb = S.activations(w, T)
-    n = min(cpu_tokens, T)
-    x, sl, wt = xb[:n], slot[:n], tw[:n]
-    w13, w2 = S.slot_tensors(w)
-    threads = default_threads()
-    forward(x, sl, wt, w13, w2, w.types[0], w.types[2], w.inter, threads)  # warm (page faults, thread pool)
+def host_info() -> dict:
+    """The host the baseline ran on: logical CPUs, the affinity set, and lscpu's model,
+    sockets, physical cores and threads per core."""
+    import subprocess
+
+    info = {"nproc": os.cpu_count()}
+    try:
+        info["affinity"] = len(os.sched_getaffinity(0))
+    except AttributeError:
+        pass
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        kv = {k.strip(): v.strip() for k, _, v in (line.partition(":") for line in out.splitlines()) if _}
+        info["model"] = kv.get("Model name")
+        sockets = int(kv.get("Socket(s)", "0") or 0)
+        per_socket = int(kv.get("Core(s) per socket", "0") or 0)
+        info["sockets"] = sockets
+        info["physical_cores"] = sockets * per_socket if sockets and per_socket else None
+        info["threads_per_core"] = int(kv.get("Thread(s) per core", "0") or 0) or None
+    except Exception:  # noqa: BLE001 - lscpu missing: the counts above still stand
+        pass
+    return info
+
+
+def _time(fn, min_seconds: float, max_seconds: float):
+    fn()  # warm (page faults, the OpenMP pool)
     reps, t0 = 0, time.perf_counter()
     while True:
-        forward(x, sl, wt, w13, w2, w.types[0], w.types[2], w.inter, threads)
+        fn()
         reps += 1
         el = time.perf_counter() - t0
         if el >= min_seconds or el * (reps + 1) / reps > max_seconds:
-            break
+            return reps, el
+
+
+def bench(S, w, cpu_tokens: int, T: int, log=print, min_seconds: float = 10.0, max_seconds: float = 30.0,
+          distinct: int = 16):
+    """The CPU expert path on this host, on the first `cpu_tokens` tokens of the T-token chunk
+    of workload `w` (same routing and activations as the GPU run), two legs of at least
+    `min_seconds` each:
+      * hot routes: the routes of the H hot experts (the GPU's share of the layer, the same
+        weights): the rate compared with the GPU (`value`);
+      * full layer: every route over all E experts (the CPU's job when no expert is on the
+        GPU), E rows of expert weights made from `distinct` quantised experts (each row its
+        own memory, so the weights stream from DRAM as E distinct experts would).
+    Returns the cpu_baseline record."""
+    ids, tw, slot, _ = S.routing(w, T)
+    xb = S.activations(w, T)
+    n = min(cpu_tokens, T)
+    x, sl, wt, lid = xb[:n], slot[:n], tw[:n], ids[:n]
+    w13, w2 = S.slot_tensors(w)
+    threads = default_threads()
+    host = host_info()
+    reps, el = _time(lambda: forward(x, sl, wt, w13, w2, w.types[0], w.types[2], w.inter, threads),
+                     min_seconds, max_seconds)
     tok_s = n * reps / el
     routes = int((sl >= 0).sum())
-    log(f"cpu baseline: {n} tokens ({routes} hot routes) x {reps} reps in {el:.1f}s on {threads} threads "
+    log(f"cpu baseline, hot routes: {n} tokens ({routes} routes) x {reps} in {el:.1f}s on {threads} threads "
         f"-> {tok_s:.1f} tok/s")
+    parts = [S.expert_weights(w, e, 0, threads) for e in range(distinct)]
+    a13 = np.stack([parts[e % distinct][0] for e in range(w.experts)])
+    a2 = np.stack([parts[e % distinct][1] for e in range(w.experts)])
+    freps, fel = _time(lambda: forward(x, lid, wt, a13, a2, w.types[0], w.types[2], w.inter, threads),
+                       min_seconds, max_seconds)
+    ftok_s = n * freps / fel
+    log(f"cpu baseline, full layer: {n} tokens ({lid.size} routes over {w.experts} experts) x {freps} in {fel:.1f}s "
+        f"-> {ftok_s:.1f} tok/s")
     return {"value": round(tok_s, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"first {n} tokens of the {T}-token chunk ({routes} hot routes), {reps} repetitions, "
-                      f"{el:.1f} s; C restatement of kt-kernel forward_many (Q8_K int8 dots, OpenMP)"}
+            "sample": f"first {n} tokens of the {T}-token chunk, hot routes only ({routes} routes over the "
+                      f"{w.hot} hot experts), {reps} repetitions in {el:.1f} s; C restatement of kt-kernel "
+                      f"forward_many (Q8_K int8 dots, OpenMP, {threads} threads)",
+            "full_layer": {"value": round(ftok_s, 1), "unit": "tokens/s", "routes": int(lid.size),
+                           "experts": w.experts, "repetitions": freps, "seconds": round(fel, 1),
+                           "weights": f"{distinct} distinct quantised experts over {w.experts} rows"},
+            "host": host}
