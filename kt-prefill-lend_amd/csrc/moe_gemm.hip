@@ -118,14 +118,17 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_scan_chunks(int32_t* __rest
 // grid (nch + 3) / 4: wave w of block b scatters the routes of chunk 4b + w to perm. Every
 // block first scans the S slot totals itself (S <= 512, two per thread) for the slots' first
 // sorted positions and first tiles (tiles of bm routes); block 0 writes seg[S+1] (route
-// offsets) and tseg[S+1] (tile offsets), and thread i of the grid writes tile_info[i] =
-// {slot, first sorted route, routes in the tile, 0} for i < tseg[S] (a GEMM block reads its
-// tile in one load; no separate launch for the slot scan).
+// offsets) and tseg[S+1] (tile offsets). The grid's threads then fill the tile table in the
+// order the GEMMs' blocks read it: position p (npos = a multiple of 8 of them) belongs to
+// XCD p % 8, and XCD x takes the contiguous range of tiles [x per, (x + 1) per), per =
+// ceil(tiles / 8), so a slot's tiles (and weights) stay in one XCD's L2. Entry p = {slot,
+// first sorted route, routes in the tile, 0}, or all zero for a position without a tile
+// (a GEMM block reads its tile in one load; no separate launch for the slot scan).
 __global__ __launch_bounds__(SORT_THREADS) void sort_scatter(const int32_t* __restrict__ slot_ids, int64_t R, int S,
                                                              const int32_t* __restrict__ hist, int64_t nch,
                                                              const int32_t* __restrict__ tot,
                                                              int32_t* __restrict__ seg, int32_t* __restrict__ tseg,
-                                                             int4* __restrict__ tile_info, int bm,
+                                                             int4* __restrict__ tile_info, int64_t npos, int bm,
                                                              int32_t* __restrict__ perm) {
   __shared__ int run[SORT_THREADS / 64][MAX_SLOTS];
   __shared__ int segl[MAX_SLOTS + 1];
@@ -148,17 +151,23 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_scatter(const int32_t* __re
     if (t == 0) { seg[S] = ta; tseg[S] = tb; }
   }
   __syncthreads();  // segl, tsegl
-  // this thread's tile (if any): its slot is the last e with tsegl[e] <= i (binary search)
-  for (int64_t i = (int64_t)blockIdx.x * SORT_THREADS + t; i < tb; i += (int64_t)gridDim.x * SORT_THREADS) {
-    int lo = 0, hi = S - 1;  // tsegl[lo] <= i < tsegl[hi + 1]
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (tsegl[mid] <= i) lo = mid;
-      else hi = mid - 1;
+  const int64_t per = ((int64_t)tb + 7) / 8;
+  for (int64_t p = (int64_t)blockIdx.x * SORT_THREADS + t; p < npos; p += (int64_t)gridDim.x * SORT_THREADS) {
+    const int64_t local = p >> 3, i = (p & 7) * per + local;
+    int4 info = int4{0, 0, 0, 0};
+    if (local < per && i < tb) {
+      // the tile's slot is the last e with tsegl[e] <= i (binary search)
+      int lo = 0, hi = S - 1;  // tsegl[lo] <= i < tsegl[hi + 1]
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (tsegl[mid] <= i) lo = mid;
+        else hi = mid - 1;
+      }
+      const int q = (int)i - tsegl[lo];
+      const int n = segl[lo + 1] - segl[lo];
+      info = int4{lo, segl[lo] + q * bm, min(bm, n - q * bm), 0};
     }
-    const int q = (int)i - tsegl[lo];
-    const int n = segl[lo + 1] - segl[lo];
-    tile_info[i] = int4{lo, segl[lo] + q * bm, min(bm, n - q * bm), 0};
+    tile_info[p] = info;
   }
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t ch = (int64_t)blockIdx.x * (SORT_THREADS / 64) + w;
@@ -243,17 +252,15 @@ constexpr int gemm_waves_per_simd() { return FJ == 8 || TYPE == GGML_Q6_K || TYP
 // spread over the sub-steps. Loads past the last step re-read the last one (clamped,
 // unused), keeping the loop branch-free.
 //
-// Epilogue: the accumulators are converted (GATEUP: silu(gate) * up) into a bf16 C tile
-// in LDS, then written out as whole rows.
+// Epilogue: the accumulators are converted (GATEUP: silu(gate) * up) into a bf16 C tile in
+// LDS over the activation buffers, then written out as whole rows (the down GEMM's rows
+// scatter to Y[perm[m]], whose indices the prologue put in LDS).
 template <int TYPE, bool GATEUP, int FJ>
 __global__ __launch_bounds__(NTHREADS, (gemm_waves_per_simd<TYPE, FJ>()))
-void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes,
-                                                         const int32_t* __restrict__ perm,
-                                                         const int32_t* __restrict__ tseg,
-                                                         const int4* __restrict__ tile_info, int S, int top_k,
-                                                         const uint8_t* __restrict__ W, int w_is_table,
-                                                         int64_t w_expert_stride, int64_t rb, int Kdim, int NI,
-                                                         int NT, int64_t nblk, uint16_t* __restrict__ out) {
+void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const int32_t* __restrict__ perm,
+                  const int4* __restrict__ tile_info, int top_k, const uint8_t* __restrict__ W, int w_is_table,
+                  int64_t w_expert_stride, int64_t rb, int Kdim, int NI, int NT, int64_t nblk,
+                  uint16_t* __restrict__ out) {
   constexpr int BM = tile_m<FJ>();
   constexpr int A_BYTES = BM * A_ROW;
   constexpr int AJ = A_BYTES / (16 * NTHREADS);  // direct loads per thread per step
@@ -262,24 +269,25 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes,
   // __shared__ variable the compiler tracks the direct buffer->LDS loads per object and
   // waits for all of them (vmcnt(0)) before every LDS read, which drains the prefetch.
   constexpr int GRID_BYTES = TYPE == GGML_IQ3_S ? 512 * 4 : 0;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[AD * A_BYTES + GRID_BYTES];
+  constexpr int OROW_BYTES = GATEUP ? 0 : BM * 4;  // down: the tile's output row indices
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[AD * A_BYTES + GRID_BYTES + OROW_BYTES];
   uint32_t* const grid_lds = (uint32_t*)(smem + AD * A_BYTES);
+  int32_t* const orow_lds = (int32_t*)(smem + AD * A_BYTES + GRID_BYTES);
   using BP = BPiece<TYPE>;
 
-  // XCD-aware order: workgroups are dealt to the 8 XCDs round-robin (pid % 8). All NT
-  // N tiles of one M tile go to the same XCD, so they share its L2 for the gathered
-  // activation rows; M tiles rotate over the XCDs. gridDim.x is a multiple of 8 * NT.
+  // XCD-aware order: workgroups are dealt to the 8 XCDs round-robin (pid % 8). Tile-table
+  // position p = (idx / NT) * 8 + pid % 8 is on XCD pid % 8, and the table gives each XCD a
+  // contiguous range of (slot-sorted) M tiles, so a slot's weights are fetched into one L2;
+  // the NT N tiles of an M tile follow each other on that XCD and share the gathered rows.
+  // gridDim.x is a multiple of 8 * NT; positions without a tile hold valid = 0.
   const int64_t pid = blockIdx.x;
   const int64_t idx = pid >> 3;
   const int mt = (int)((idx / NT) * 8 + (pid & 7));
   const int nt = (int)(idx % NT);
   if ((int64_t)mt * NT + nt >= nblk) return;
-  // the tile count and the tile's description in parallel (mt < max_tiles: in bounds; the
-  // entries past the count are stale and unused)
-  const int ntiles = tseg[S];
   const int4 ti = tile_info[mt];
-  if (mt >= ntiles) return;
   const int e = ti.x, m0 = ti.y, valid = ti.z;
+  if (valid == 0) return;
 
   if constexpr (TYPE == GGML_IQ3_S) stage_iq3s_grid(grid_lds);
 
@@ -301,6 +309,11 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes,
     if constexpr (GATEUP) src_row = perm[m0 + r] / top_k;
     else src_row = m0 + r;
     a_off[j] = 2u * (uint32_t)(src_row * Kdim + BP::coff(chunk));
+  }
+  // down: the output row of each of the tile's routes (-1 past its routes), in LDS (visible
+  // after the prologue's barrier, read by the epilogue)
+  if constexpr (!GATEUP) {
+    for (int ml = tid; ml < BM; ml += NTHREADS) orow_lds[ml] = ml < valid ? perm[m0 + ml] : -1;
   }
   // buffer loads into LDS: the step's column offset is a scalar operand, the lane's row
   // offset a fixed register, so no address arithmetic per load; reads beyond a_bytes
@@ -354,7 +367,7 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes,
   typename BP::Raw raw[2][FI];
   typename BP::Head head[FI], head_nxt[FI];  // super-block sb's shared bytes, and sb+1's
   uint32_t wv[2][FI][16];
-  const int nsb = Kdim / 256;  // super-block columns, 4 steps each
+  const int nsb = Kdim / 256;  // super-block columns per tile, 4 steps each
   const int lsb = nsb - 1;
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, 1>;
@@ -363,22 +376,26 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes,
 
   // prologue in the steady state's issue order (step j issues A(j+3), then raw(j+2)):
   // A(0), A(1), raw(0), A(2), raw(1), so that at the end of step 0 as many loads follow
-  // A(1) as at any later step; then wait for A(0) only and decode step 0 (its raw bytes
-  // come after A(1): the compiler's wait for them also covers A(1))
-  // (sched_barrier keeps the compiler from hoisting the register loads above the direct ones)
+  // A(1) as at any later step (sched_barrier keeps the compiler from hoisting the register
+  // loads above the direct ones)
+  auto prologue = [&]() {
 #pragma unroll
-  for (int i = 0; i < FI; ++i) BP::load_head(b_row[i], 0, h, head[i]);
-  issue_a(0, S0{}, 0, 0, AJ);
-  issue_a(0, S1{}, 1, 0, AJ);
-  __builtin_amdgcn_sched_barrier(0);
+    for (int i = 0; i < FI; ++i) BP::load_head(b_row[i], 0, h, head[i]);
+    issue_a(0, S0{}, 0, 0, AJ);
+    issue_a(0, S1{}, 1, 0, AJ);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int i = 0; i < FI; ++i) BP::template load<0>(b_row[i], 0, h, grid_lds, raw[0][i]);
-  __builtin_amdgcn_sched_barrier(0);
-  issue_a(0, S2{}, 2, 0, AJ);
-  __builtin_amdgcn_sched_barrier(0);
+    for (int i = 0; i < FI; ++i) BP::template load<0>(b_row[i], 0, h, grid_lds, raw[0][i]);
+    __builtin_amdgcn_sched_barrier(0);
+    issue_a(0, S2{}, 2, 0, AJ);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int i = 0; i < FI; ++i) BP::template load<1>(b_row[i], 0, h, grid_lds, raw[1][i]);
-  __builtin_amdgcn_sched_barrier(0);
+    for (int i = 0; i < FI; ++i) BP::template load<1>(b_row[i], 0, h, grid_lds, raw[1][i]);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  prologue();
+  // wait for A(0) only and decode step 0 (its raw bytes come after A(1): the compiler's wait
+  // for them also covers A(1))
   static_assert(2 * AJ + 2 * FI * BP::NLOAD < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt(wait_vmcnt(2 * AJ + 2 * FI * BP::NLOAD));
   __syncthreads();  // A(0) of every wave; the codebook
@@ -441,7 +458,7 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes,
       // schedule: the direct loads first, then 32 x (1 MFMA, VPM VALU), an LDS read after
       // every other MFMA and one of the raw weight gathers after every other (each
       // gathers 32 rows' cache lines: in one burst they would hold up the MFMA issue).
-      // VPM covers the type's decode (Q4_K and Q8_0 about 3.5 VALU per MFMA, Q6_K 6,
+      // VPM covers the type's decode (Q4_K and Q8_0 about 3.5 VALU per MFMA, Q6_K 4.3,
       // IQ3_S 7): VALU left over would run after the last MFMA with the matrix core idle.
       __builtin_amdgcn_sched_group_barrier(0x020, AJ / 2, 0);
 #pragma unroll
@@ -467,20 +484,13 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes,
       for (int i = 0; i < FI; ++i) head[i] = head_nxt[i];
     }
   };
-  for (int sb = 0; sb < nsb; ++sb) {
-    step(sb, S0{});
-    step(sb, S1{});
-    step(sb, S2{});
-    step(sb, S3{});
-  }
-  __builtin_amdgcn_s_waitcnt(0);  // the clamped prefetches of the last steps
-  __syncthreads();                 // every wave is done with the activation buffers
 
-  // ---- epilogue: the bf16 C tile is staged in LDS (rows of CW 16-byte chunks, chunk c of
-  // row r at slot c ^ (r % CW)), then written out as whole rows, 16 bytes per lane.
+  // The bf16 C tile is staged in LDS over the activation buffers (rows of CW 16-byte
+  // chunks, chunk c of row r at slot c ^ (r % CW)), then written out as whole rows, 16 bytes
+  // per lane (each row's segment by consecutive lanes: full cache lines per instruction).
   // Accumulator layout: lane l holds route 32 j + l % 32 and weight rows
   // 8 (r / 4) + 4 (l / 32) + r % 4 of fragment i: 4 consecutive columns per (i, j, r / 4).
-  constexpr int CCOLS = GATEUP ? BNW / 2 : BNW;  // output columns of the tile
+  constexpr int CCOLS = GATEUP ? BNW / 2 : BNW;  // output columns of a tile
   constexpr int CW = CCOLS / 8;                  // 16-byte chunks per row
   static_assert(BM * CCOLS * 2 <= AD * A_BYTES, "C tile fits the activation buffers");
   uint8_t* cs = smem;
@@ -489,60 +499,81 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes,
     u32x2_t v = {lo, hi};
     *(u32x2_t*)(cs + row * (CW * 16) + 16 * (c ^ (row % CW)) + 2 * (col & 7)) = v;
   };
-  if constexpr (GATEUP) {
-    constexpr int FH = FI / 2;
+  constexpr int NIT = BM * CW / NTHREADS;
+  static_assert(BM * CW % NTHREADS == 0, "store mapping");
+
+  // down: the accumulators to the bf16 output rows Y[perm[m]] (streamed past the caches: Y is
+  // read once, by the combine, long after)
+  auto flush = [&]() {
+    if constexpr (!GATEUP) {
+      __builtin_amdgcn_s_waitcnt(0);  // the clamped prefetches of the last steps (into LDS)
+      __syncthreads();                 // every wave is done with the activation buffers
 #pragma unroll
-    for (int j = 0; j < FJ; ++j) {
-      const int ml = 32 * (wm * FJ + j) + l32;
+      for (int j = 0; j < FJ; ++j) {
+        const int ml = 32 * (wm * FJ + j) + l32;
 #pragma unroll
-      for (int i = 0; i < FH; ++i)
+        for (int i = 0; i < FI; ++i) {
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-          const f32x16_t& g = acc[i][j];
-          const f32x16_t& u = acc[i + FH][j];
-          c_put(ml, (wn * FH + i) * 32 + 8 * r4 + 4 * h,
-                f2bf2(silu_mul(g[4 * r4], u[4 * r4]), silu_mul(g[4 * r4 + 1], u[4 * r4 + 1])),
-                f2bf2(silu_mul(g[4 * r4 + 2], u[4 * r4 + 2]), silu_mul(g[4 * r4 + 3], u[4 * r4 + 3])));
+          for (int r4 = 0; r4 < 4; ++r4) {
+            const f32x16_t& a = acc[i][j];
+            c_put(ml, (wn * FI + i) * 32 + 8 * r4 + 4 * h, f2bf2(a[4 * r4], a[4 * r4 + 1]),
+                  f2bf2(a[4 * r4 + 2], a[4 * r4 + 3]));
+          }
         }
-    }
-  } else {
+      }
+      __syncthreads();
+      const int64_t col0 = (int64_t)nt * CCOLS;
 #pragma unroll
-    for (int j = 0; j < FJ; ++j) {
-      const int ml = 32 * (wm * FJ + j) + l32;
-#pragma unroll
-      for (int i = 0; i < FI; ++i)
-#pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-          const f32x16_t& a = acc[i][j];
-          c_put(ml, (wn * FI + i) * 32 + 8 * r4 + 4 * h, f2bf2(a[4 * r4], a[4 * r4 + 1]),
-                f2bf2(a[4 * r4 + 2], a[4 * r4 + 3]));
+      for (int it = 0; it < NIT; ++it) {
+        const int qq = tid + it * NTHREADS;
+        const int ml = qq / CW, c = qq % CW;
+        const int orow = orow_lds[ml];
+        if (orow >= 0) {
+          const u32x4_t v = *(const u32x4_t*)(cs + ml * (CW * 16) + 16 * (c ^ (ml % CW)));
+          __builtin_nontemporal_store(v, (u32x4_t*)(out + (int64_t)orow * NI + col0 + 8 * c));
         }
+      }
     }
+  };
+
+  for (int sb = 0; sb < nsb; ++sb) {
+    step(sb, S0{});
+    step(sb, S1{});
+    step(sb, S2{});
+    step(sb, S3{});
+  }
+  if constexpr (!GATEUP) {
+    flush();
+    return;
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the clamped prefetches of the last steps
+  __syncthreads();                 // every wave is done with the activation buffers
+
+  // ---- gate/up epilogue: silu(gate) * up into the C tile, then whole rows of H
+  constexpr int FH = FI / 2;
+#pragma unroll
+  for (int j = 0; j < FJ; ++j) {
+    const int ml = 32 * (wm * FJ + j) + l32;
+#pragma unroll
+    for (int i = 0; i < FH; ++i)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const f32x16_t& g = acc[i][j];
+        const f32x16_t& u = acc[i + FH][j];
+        c_put(ml, (wn * FH + i) * 32 + 8 * r4 + 4 * h,
+              f2bf2(silu_mul(g[4 * r4], u[4 * r4]), silu_mul(g[4 * r4 + 1], u[4 * r4 + 1])),
+              f2bf2(silu_mul(g[4 * r4 + 2], u[4 * r4 + 2]), silu_mul(g[4 * r4 + 3], u[4 * r4 + 3])));
+      }
   }
   __syncthreads();
   const int64_t col0 = (int64_t)nt * CCOLS;
-  // every output row index of this thread first (the down GEMM's rows scatter through perm:
-  // one round of loads rather than one per store), then the stores, unrolled
-  constexpr int NIT = BM * CW / NTHREADS;
-  static_assert(BM * CW % NTHREADS == 0, "store mapping");
-  int orow[NIT];
-#pragma unroll
-  for (int it = 0; it < NIT; ++it) {
-    const int ml = (tid + it * NTHREADS) / CW;
-    orow[it] = ml < valid ? (GATEUP ? m0 + ml : perm[m0 + ml]) : -1;
-  }
 #pragma unroll
   for (int it = 0; it < NIT; ++it) {
     const int q = tid + it * NTHREADS;
     const int ml = q / CW, c = q % CW;
-    if (orow[it] >= 0) {
+    if (ml < valid) {
       const u32x4_t v = *(const u32x4_t*)(cs + ml * (CW * 16) + 16 * (c ^ (ml % CW)));
-      if constexpr (GATEUP) {
-        *(u32x4_t*)(out + (int64_t)orow[it] * NI + col0 + 8 * c) = v;  // read back by the down GEMM
-      } else {
-        // Y is read once, by the combine, long after: streamed past the caches
-        __builtin_nontemporal_store(v, (u32x4_t*)(out + (int64_t)orow[it] * NI + col0 + 8 * c));
-      }
+      *(u32x4_t*)(out + (int64_t)(m0 + ml) * NI + col0 + 8 * c) = v;  // read back by the down GEMM
     }
   }
 }
@@ -578,34 +609,34 @@ __global__ __launch_bounds__(256) void combine_routes(const uint16_t* __restrict
 
 template <int TYPE, bool GATEUP, int FJ>
 void launch_gemm(dim3 grid, hipStream_t stream, const uint16_t* A_src, uint32_t a_bytes, const int32_t* perm,
-                 const int32_t* tseg, const int4* tile_info, int S, int top_k, const void* W, int w_is_table, int64_t w_expert_stride,
-                 int64_t rb, int Kdim, int NI, int NT, int64_t nblk, uint16_t* out) {
-  grouped_gemm<TYPE, GATEUP, FJ><<<grid, NTHREADS, 0, stream>>>(A_src, a_bytes, perm, tseg, tile_info, S, top_k, (const uint8_t*)W,
-                                                             w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out);
+                 const int4* tile_info, int top_k, const void* W, int w_is_table, int64_t w_expert_stride, int64_t rb,
+                 int Kdim, int NI, int NT, int64_t nblk, uint16_t* out) {
+  grouped_gemm<TYPE, GATEUP, FJ><<<grid, NTHREADS, 0, stream>>>(A_src, a_bytes, perm, tile_info, top_k,
+                                                               (const uint8_t*)W, w_is_table, w_expert_stride, rb,
+                                                               Kdim, NI, NT, nblk, out);
 }
 
 template <bool GATEUP, int TYPE>
-void launch_fj(int fj, dim3 grid, hipStream_t stream, const uint16_t* A_src, uint32_t a_bytes, const int32_t* perm,
-               const int32_t* tseg, const int4* tile_info, int S, int top_k, const void* W, int w_is_table,
+void launch_fj(int fj, dim3 grid, hipStream_t stream, const uint16_t* A_src, uint32_t a_bytes,
+               const int32_t* perm, const int4* tile_info, int top_k, const void* W, int w_is_table,
                int64_t w_expert_stride, int64_t rb, int Kdim, int NI, int NT, int64_t nblk, uint16_t* out) {
   if (fj == 8)
-    launch_gemm<TYPE, GATEUP, 8>(grid, stream, A_src, a_bytes, perm, tseg, tile_info, S, top_k, W, w_is_table,
+    launch_gemm<TYPE, GATEUP, 8>(grid, stream, A_src, a_bytes, perm, tile_info, top_k, W, w_is_table,
                                  w_expert_stride, rb, Kdim, NI, NT, nblk, out);
   else
-    launch_gemm<TYPE, GATEUP, 4>(grid, stream, A_src, a_bytes, perm, tseg, tile_info, S, top_k, W, w_is_table,
+    launch_gemm<TYPE, GATEUP, 4>(grid, stream, A_src, a_bytes, perm, tile_info, top_k, W, w_is_table,
                                  w_expert_stride, rb, Kdim, NI, NT, nblk, out);
 }
 
 template <bool GATEUP>
 int dispatch_gemm(int type, int fj, dim3 grid, hipStream_t stream, const uint16_t* A_src, uint32_t a_bytes,
-                  const int32_t* perm,
-                  const int32_t* tseg, const int4* tile_info, int S, int top_k, const void* W, int w_is_table,
+                  const int32_t* perm, const int4* tile_info, int top_k, const void* W, int w_is_table,
                   int64_t w_expert_stride, int64_t rb, int Kdim, int NI, int NT, int64_t nblk, uint16_t* out) {
   switch (type) {
-    case GGML_Q8_0: launch_fj<GATEUP, GGML_Q8_0>(fj, grid, stream, A_src, a_bytes, perm, tseg, tile_info, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
-    case GGML_Q4_K: launch_fj<GATEUP, GGML_Q4_K>(fj, grid, stream, A_src, a_bytes, perm, tseg, tile_info, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
-    case GGML_Q6_K: launch_fj<GATEUP, GGML_Q6_K>(fj, grid, stream, A_src, a_bytes, perm, tseg, tile_info, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
-    case GGML_IQ3_S: launch_fj<GATEUP, GGML_IQ3_S>(fj, grid, stream, A_src, a_bytes, perm, tseg, tile_info, S, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
+    case GGML_Q8_0: launch_fj<GATEUP, GGML_Q8_0>(fj, grid, stream, A_src, a_bytes, perm, tile_info, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
+    case GGML_Q4_K: launch_fj<GATEUP, GGML_Q4_K>(fj, grid, stream, A_src, a_bytes, perm, tile_info, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
+    case GGML_Q6_K: launch_fj<GATEUP, GGML_Q6_K>(fj, grid, stream, A_src, a_bytes, perm, tile_info, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
+    case GGML_IQ3_S: launch_fj<GATEUP, GGML_IQ3_S>(fj, grid, stream, A_src, a_bytes, perm, tile_info, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
     default: set_error("grouped GEMM: ggml type %d has no kernel", type); return KTMI_ETYPE;
   }
   KTMI_HIP_TRY(hipGetLastError());
@@ -633,7 +664,7 @@ GroupedPlan grouped_plan(int64_t tokens, int64_t top_k, int64_t n_slots, int64_t
   P.fj = grouped_fj(P.routes, n_slots, inter);
   P.bm = 32 * WM * P.fj;
   const int64_t nch = (P.routes + CHW - 1) / CHW;
-  P.max_tiles = (P.routes + P.bm - 1) / P.bm + n_slots;
+  P.max_tiles = ((P.routes + P.bm - 1) / P.bm + n_slots + 7) / 8 * 8;  // tile-table positions, 8 per XCD round
   int64_t o = 0;
   P.off_counts = o; o = align256(o + ((nch > 0 ? nch : 1) * n_slots + n_slots) * 4);
   P.off_seg = o; o = align256(o + (n_slots + 1) * 4);
@@ -673,8 +704,8 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
   record_stage(0, stream);
   sort_count<<<sblocks, SORT_THREADS, 0, stream>>>(slot_ids, R, S, hist, nch);
   sort_scan_chunks<<<S, SORT_THREADS, 0, stream>>>(hist, nch, tot);
-  sort_scatter<<<sblocks, SORT_THREADS, 0, stream>>>(slot_ids, R, S, hist, nch, tot, seg, tseg, tile_info, (int)P.bm,
-                                                     perm);
+  sort_scatter<<<sblocks, SORT_THREADS, 0, stream>>>(slot_ids, R, S, hist, nch, tot, seg, tseg, tile_info,
+                                                     P.max_tiles, (int)P.bm, perm);
   KTMI_HIP_TRY(hipGetLastError());
   record_stage(1, stream);
   const int64_t rb13 = row_bytes(K, L->type13), rb2 = row_bytes(N, L->type2);
@@ -682,16 +713,16 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
   const int NT1 = (int)(N / (BNW / 2));
   const int64_t nblk1 = P.max_tiles * NT1;
   dim3 g1((unsigned)((nblk1 + 8 * NT1 - 1) / (8 * NT1) * (8 * NT1)));
-  int rc = dispatch_gemm<true>(L->type13, P.fj, g1, stream, x, (uint32_t)(tokens * K * 2), perm, tseg, tile_info, S, (int)top_k, L->w13, L->w_is_table,
-                               st13, rb13, (int)K, (int)N, NT1, nblk1, H);
+  int rc = dispatch_gemm<true>(L->type13, P.fj, g1, stream, x, (uint32_t)(tokens * K * 2), perm, tile_info,
+                               (int)top_k, L->w13, L->w_is_table, st13, rb13, (int)K, (int)N, NT1, nblk1, H);
   if (rc) return rc;
   record_stage(2, stream);  // no mid stage on this path: SiLU*mul is in the gate/up epilogue
   record_stage(3, stream);
   const int NT2 = (int)(K / BNW);
   const int64_t nblk2 = P.max_tiles * NT2;
   dim3 g2((unsigned)((nblk2 + 8 * NT2 - 1) / (8 * NT2) * (8 * NT2)));
-  rc = dispatch_gemm<false>(L->type2, P.fj, g2, stream, H, (uint32_t)(R * N * 2), perm, tseg, tile_info, S, (int)top_k, L->w2, L->w_is_table, st2, rb2,
-                            (int)N, (int)K, NT2, nblk2, Y);
+  rc = dispatch_gemm<false>(L->type2, P.fj, g2, stream, H, (uint32_t)(R * N * 2), perm, tile_info, (int)top_k,
+                            L->w2, L->w_is_table, st2, rb2, (int)N, (int)K, NT2, nblk2, Y);
   if (rc) return rc;
   record_stage(4, stream);
   for (int64_t t0 = 0; t0 < tokens; t0 += 65535) {

@@ -59,6 +59,7 @@ def test_decode_gate_up_counted_wait_covers_the_weight_loads(tmp_path):
 
 
 def _k_loop(lines, st, end):
+    """The innermost loop holding the most MFMAs (the super-block loop)."""
     labels = {}
     for i in range(st, end):
         m = re.match(r"^(\.LBB\w+):", lines[i])
@@ -69,8 +70,9 @@ def _k_loop(lines, st, end):
         m = re.search(r"s_cbranch_\w+\s+(\.LBB\w+)", lines[i])
         if m and m.group(1) in labels and labels[m.group(1)] < i:
             loops.append((labels[m.group(1)], i))
-    # the super-block loop is the one holding the MFMAs
-    return max(loops, key=lambda ab: sum("v_mfma" in lines[j] for j in range(ab[0], ab[1])))
+    count = {ab: sum("v_mfma" in lines[j] for j in range(ab[0], ab[1])) for ab in loops}
+    most = max(count.values())
+    return min((ab for ab in loops if count[ab] == most), key=lambda ab: ab[1] - ab[0])
 
 
 def test_grouped_gemm_counted_waits_cover_the_activation_tiles(tmp_path):
