@@ -352,12 +352,13 @@ def decode_floor(torch, ev, dev, nbytes, ncopy, steps):
             "two_launches_ms": round(launch_ms, 4)}
 
 
-def bench_hybrid(P, torch, S, ev, dev, distinct=16, reps=100, warmup=5):
+def bench_hybrid(P, torch, S, ev, dev, distinct=16, reps=200, warmup=10):
     """The whole decode layer of the decode workload (256 experts, 32 hot on the GPU, Q4_K)
     at 1 / 4 / 16 tokens: the hot routes on the GPU (GEMV mode), the cold ones on the host
     cores through the library's CPU engine and handoff (submit before the GPU kernels,
-    sync_add after). Per step (host clock, reps steps): GPU half alone, CPU half alone
-    (engine forward on host arrays), and the hybrid layer; the CPU engine's rate is the
+    sync_add after). Per step (host clock, median of reps synchronised steps): GPU half
+    alone, CPU half alone (engine forward on host arrays), and the hybrid layer; the CPU
+    engine's rate is the
     bytes of the distinct cold experts it read per step. Experts: `distinct` quantised
     experts copied over the 256 bank rows (every row is its own memory)."""
     H, L = P.kt_gguf_hot, P._lib
@@ -378,14 +379,18 @@ def bench_hybrid(P, torch, S, ev, dev, distinct=16, reps=100, warmup=5):
     res = {"workload": w.name, "cpu_threads": cpu.threads, "cpu_isa": cpu.isa}
 
     def clock(fn):
+        # per-step host-clock times, each step ending in a device synchronisation; the median
+        # (the shared host's scheduling hiccups land in the tail)
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
+        ts = []
         for _ in range(reps):
+            t0 = time.perf_counter()
             fn()
-        torch.cuda.synchronize()
-        return (time.perf_counter() - t0) * 1e3 / reps
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts)) * 1e3
 
     for T in (1, 4, 16):
         ids, tw, slot, _ = S.routing(w, T)

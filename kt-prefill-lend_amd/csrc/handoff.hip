@@ -4,8 +4,10 @@
 //
 // submit(x, ids, weights) on the compute stream: one kernel writes them into the engine's
 // pinned staging buffers through their device addresses (the reference's UVA staging,
-// kt_uva_handoff._stage_kernel; one launch instead of three small copies), then an event; the engine's worker thread waits for the
-// event, runs the cold routes on the host cores (cpu_moe.cpp) into a pinned bf16 output.
+// kt_uva_handoff._stage_kernel; one launch instead of three small copies) and publishes the
+// submit's sequence number in pinned memory once all its blocks' writes are visible; the
+// engine's worker thread spins on that number (an event on the stream is the fallback),
+// runs the cold routes on the host cores (cpu_moe.cpp) into a pinned bf16 output.
 // The stream goes on with the GPU's hot experts meanwhile. sync_add(out): the host spins
 // until the worker is done, then out = bf16(out + cpu) on the stream (the wrapper's
 // `output + cpu_output`), the add kernel reading the CPU output from pinned memory through
@@ -34,6 +36,13 @@ struct ktmi_cpu_moe {
   int32_t* ids_hd = nullptr;
   float* w_hd = nullptr;
   uint16_t* out_hd = nullptr;
+  // staging handshake: the staging kernel's last block stores the submit's sequence number
+  // into pinned memory (seq_h, device address seq_hd) after every block's writes; blocks_d
+  // counts the blocks done (device memory, reset by the last block)
+  uint32_t* seq_h = nullptr;
+  uint32_t* seq_hd = nullptr;
+  uint32_t* blocks_d = nullptr;
+  uint32_t seq = 0;
   hipEvent_t in_ready = nullptr, out_free = nullptr;
   bool out_free_pending = false;
   std::thread worker;
@@ -48,16 +57,31 @@ struct ktmi_cpu_moe {
 
 namespace {
 
-// x [T, K] bf16 (16-byte chunks), ids and weights [P] into pinned host memory
+// x [T, K] bf16 (16-byte chunks), ids and weights [P] into pinned host memory; then the
+// last block to finish publishes `seq` in pinned memory: every block makes its writes
+// visible to the host (system-scope fence) before it counts itself done, and the block that
+// counts last stores seq with system-scope release (and resets the counter for the next
+// submit, which the stream orders after this kernel)
 __global__ __launch_bounds__(256) void stage_kernel(const u32x4_t* __restrict__ x, int64_t nx,
                                                      const int32_t* __restrict__ ids, const float* __restrict__ w,
                                                      int64_t P, u32x4_t* __restrict__ xh, int32_t* __restrict__ idsh,
-                                                     float* __restrict__ wh) {
+                                                     float* __restrict__ wh, uint32_t* blocks_done,
+                                                     uint32_t* seq_out, uint32_t seq) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nx; i += stride) xh[i] = x[i];
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < P; i += stride) {
     idsh[i] = ids[i];
     wh[i] = w[i];
+  }
+  __threadfence_system();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t done = atomicAdd(blocks_done, 1u);
+    if (done == gridDim.x - 1) {
+      __threadfence_system();
+      *blocks_done = 0;
+      __hip_atomic_store(seq_out, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
   }
 }
 
@@ -86,12 +110,27 @@ int event_wait(hipEvent_t e) {
   return hipEventSynchronize(e) == hipSuccess ? 0 : -2;
 }
 
+// the staged inputs of submit `seq` are in pinned memory: spin on the sequence number the
+// staging kernel publishes (no runtime call on the way); past `spin_us` fall back to the
+// stream event, which also reports a failed stream instead of waiting for ever
+int staged_wait(ktmi_cpu_moe* h, uint32_t seq, int spin_us) {
+  const auto t0 = std::chrono::steady_clock::now();
+  for (int i = 0;; ++i) {
+    if ((int32_t)(__atomic_load_n(h->seq_h, __ATOMIC_ACQUIRE) - seq) >= 0) return 0;
+    _mm_pause();
+    if ((i & 63) == 63 && std::chrono::steady_clock::now() - t0 > std::chrono::microseconds(spin_us)) break;
+  }
+  const int rc = event_wait(h->in_ready);
+  if (rc) return rc;
+  return (int32_t)(__atomic_load_n(h->seq_h, __ATOMIC_ACQUIRE) - seq) >= 0 ? 0 : -3;
+}
+
 void worker_loop(ktmi_cpu_moe* h) {
   (void)hipSetDevice(h->device);
   for (;;) {
     wait_for(h, [h] { return h->stop || h->state.load() == ktmi_cpu_moe::SUBMITTED; }, 50);
     if (h->stop) return;
-    int rc = event_wait(h->in_ready);
+    int rc = staged_wait(h, h->seq, 2000);
     if (rc == 0 && h->out_free_pending) rc = event_wait(h->out_free);
     if (rc == 0) rc = ktmi_cpu::engine_forward(h->eng, h->T, h->k, h->ids_h, h->w_h, h->x_h, h->out_h);
     h->rc = rc;
@@ -122,6 +161,8 @@ void destroy(ktmi_cpu_moe* h) {
   if (h->ids_h) (void)hipHostFree(h->ids_h);
   if (h->w_h) (void)hipHostFree(h->w_h);
   if (h->out_h) (void)hipHostFree(h->out_h);
+  if (h->seq_h) (void)hipHostFree(h->seq_h);
+  if (h->blocks_d) (void)hipFree(h->blocks_d);
   ktmi_cpu::engine_destroy(h->eng);
   delete h;
 }
@@ -174,6 +215,12 @@ ktmi_cpu_moe* ktmi_cpu_moe_create(int64_t hidden, int64_t inter, int type13, int
     if (e == hipSuccess) e = hipHostGetDevicePointer((void**)&h->ids_hd, h->ids_h, 0);
     if (e == hipSuccess) e = hipHostGetDevicePointer((void**)&h->w_hd, h->w_h, 0);
     if (e == hipSuccess) e = hipHostGetDevicePointer((void**)&h->out_hd, h->out_h, 0);
+    if (e == hipSuccess) e = hipHostMalloc((void**)&h->seq_h, 64, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipHostGetDevicePointer((void**)&h->seq_hd, h->seq_h, 0);
+    if (e == hipSuccess) e = hipMalloc((void**)&h->blocks_d, 4);
+    if (e == hipSuccess) e = hipMemset(h->blocks_d, 0, 4);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e == hipSuccess) __atomic_store_n(h->seq_h, 0u, __ATOMIC_RELEASE);
   }
   if (e != hipSuccess) {
     set_error("cpu_moe_create: %s", hipGetErrorString(e));
@@ -233,8 +280,10 @@ int ktmi_cpu_moe_submit(ktmi_cpu_moe* h, const void* x_bf16, const int32_t* expe
   hipStream_t s = (hipStream_t)stream;
   const int64_t nx = tokens * h->K / 8, P = tokens * top_k;  // K is a multiple of 256
   const int64_t blocks = std::min<int64_t>(((nx > P ? nx : P) + 255) / 256, 1024);
+  h->seq += 1;
   stage_kernel<<<(unsigned)blocks, 256, 0, s>>>((const u32x4_t*)x_bf16, nx, expert_ids, weights, P,
-                                                (u32x4_t*)h->x_hd, h->ids_hd, h->w_hd);
+                                                (u32x4_t*)h->x_hd, h->ids_hd, h->w_hd, h->blocks_d, h->seq_hd,
+                                                h->seq);
   KTMI_HIP_TRY(hipGetLastError());
   KTMI_HIP_TRY(hipEventRecord(h->in_ready, s));
   h->state = ktmi_cpu_moe::SUBMITTED;
