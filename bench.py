@@ -352,15 +352,18 @@ def decode_floor(torch, ev, dev, nbytes, ncopy, steps):
             "two_launches_ms": round(launch_ms, 4)}
 
 
-def bench_hybrid(P, torch, S, ev, dev, distinct=16, reps=200, warmup=10):
+def bench_hybrid(P, torch, S, ev, dev, distinct=16, reps=200, warmup=10, rotate=8):
     """The whole decode layer of the decode workload (256 experts, 32 hot on the GPU, Q4_K)
     at 1 / 4 / 16 tokens: the hot routes on the GPU (GEMV mode), the cold ones on the host
     cores through the library's CPU engine and handoff (submit before the GPU kernels,
-    sync_add after). Per step (host clock, median of reps synchronised steps): GPU half
-    alone, CPU half alone (engine forward on host arrays), and the hybrid layer; the CPU
-    engine's rate is the
-    bytes of the distinct cold experts it read per step. Experts: `distinct` quantised
-    experts copied over the 256 bank rows (every row is its own memory)."""
+    sync_add after). Per step (host clock from the first call to the device synchronisation,
+    median over reps): GPU half alone, CPU half alone (engine forward on host arrays) and the
+    hybrid layer, the three legs interleaved step by step so that they see the same state
+    of the shared host. The calls cycle through `rotate` routings (other seeds), one further
+    per call, so the cold experts a call reads were last read `rotate` calls before (their
+    union is reported) rather than staying in the host's caches; the CPU engine's rate is
+    the bytes of the distinct cold experts a call reads over the CPU-alone time. Experts: `distinct` quantised experts
+    copied over the 256 bank rows (every row is its own memory)."""
     H, L = P.kt_gguf_hot, P._lib
     import kt_prefill_lend_amd.kt_cpu_moe as CM
     from kt_prefill_lend_amd.gguf import row_bytes
@@ -376,44 +379,66 @@ def bench_hybrid(P, torch, S, ev, dev, distinct=16, reps=200, warmup=10):
     W13, W2 = torch.from_numpy(w13).to(dev), torch.from_numpy(w2).to(dev)
     desc = H.layer_desc(W13, W2, K, N, w.types[0], w.types[2])
     exp_bytes = 2 * N * row_bytes(K, w.types[0]) + K * row_bytes(N, w.types[2])
-    res = {"workload": w.name, "cpu_threads": cpu.threads, "cpu_isa": cpu.isa}
+    res = {"workload": w.name, "cpu_threads": cpu.threads, "cpu_isa": cpu.isa, "routings": rotate}
 
-    def clock(fn):
-        # per-step host-clock times, each step ending in a device synchronisation; the median
-        # (the shared host's scheduling hiccups land in the tail)
+    def clock(legs):
+        # a step runs every leg once, each ending in a device synchronisation; every call
+        # takes the next routing, so whatever a leg reads was last read `rotate` calls
+        # before, by any leg; per-leg medians (the shared host's hiccups land in the tail)
+        c = 0
         for _ in range(warmup):
-            fn()
+            for f in legs:
+                f(c)
+                c += 1
         torch.cuda.synchronize()
-        ts = []
+        ts = [[] for _ in legs]
         for _ in range(reps):
-            t0 = time.perf_counter()
-            fn()
-            torch.cuda.synchronize()
-            ts.append(time.perf_counter() - t0)
-        return float(np.median(ts)) * 1e3
+            for j, f in enumerate(legs):
+                t0 = time.perf_counter()
+                f(c)
+                torch.cuda.synchronize()
+                ts[j].append(time.perf_counter() - t0)
+                c += 1
+        return [float(np.median(t)) * 1e3 for t in ts]
 
     for T in (1, 4, 16):
-        ids, tw, slot, _ = S.routing(w, T)
-        cold = np.where(slot < 0, ids, -1).astype(np.int32)
-        xb = S.activations(w, T)
-        x = torch.from_numpy(xb.view(np.int16)).to(dev).view(torch.bfloat16)
-        x_h = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16)
-        tw_d, slot_d, cold_d = torch.from_numpy(tw).to(dev), torch.from_numpy(slot).to(dev), torch.from_numpy(cold).to(dev)
-        cold_h, tw_h = torch.from_numpy(cold), torch.from_numpy(tw)
+        rs = []
+        for r in range(rotate):
+            wr = S.small(w, index=w.index + 1000 * r)  # another routing and x per rotation
+            ids, tw, slot, _ = S.routing(wr, T)
+            cold = np.where(slot < 0, ids, -1).astype(np.int32)
+            xb = S.activations(wr, T)
+            rs.append(dict(
+                x=torch.from_numpy(xb.view(np.int16)).to(dev).view(torch.bfloat16),
+                x_h=torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16),
+                tw_d=torch.from_numpy(tw).to(dev), slot_d=torch.from_numpy(slot).to(dev),
+                cold_d=torch.from_numpy(cold).to(dev), cold_h=torch.from_numpy(cold), tw_h=torch.from_numpy(tw),
+                hot=int((slot >= 0).sum()), n_cold=int((cold >= 0).sum()), cold_set=set(cold[cold >= 0].tolist())))
         out = torch.empty((T, K), dtype=torch.bfloat16, device=dev)
         ws = torch.empty((L.lib().ktmi_moe_layer_workspace(desc, T, w.top_k, L.MODE_GEMV),), dtype=torch.uint8, device=dev)
-        gpu_ms = clock(lambda: H.moe_layer(desc, x, tw_d, slot_d, L.MODE_GEMV, out, ws))
-        cpu_ms = clock(lambda: cpu.forward(x_h, cold_h, tw_h))
 
-        def hybrid():
-            cpu.submit(x, cold_d, tw_d)
-            H.moe_layer(desc, x, tw_d, slot_d, L.MODE_GEMV, out, ws)
+        def gpu_half(i):
+            d = rs[i % rotate]
+            H.moe_layer(desc, d["x"], d["tw_d"], d["slot_d"], L.MODE_GEMV, out, ws)
+
+        def cpu_half(i):
+            d = rs[i % rotate]
+            cpu.forward(d["x_h"], d["cold_h"], d["tw_h"])
+
+        def hybrid(i):
+            d = rs[i % rotate]
+            cpu.submit(d["x"], d["cold_d"], d["tw_d"])
+            H.moe_layer(desc, d["x"], d["tw_d"], d["slot_d"], L.MODE_GEMV, out, ws)
             cpu.sync_add(out)
 
-        hy_ms = clock(hybrid)
-        n_cold = len(set(cold[cold >= 0].tolist()))
-        r = {"hot_routes": int((slot >= 0).sum()), "cold_routes": int((cold >= 0).sum()), "cold_experts": n_cold,
+        gpu_ms, cpu_ms, hy_ms = clock([gpu_half, cpu_half, hybrid])
+        n_cold = float(np.mean([len(d["cold_set"]) for d in rs]))
+        union = set().union(*[d["cold_set"] for d in rs])
+        r = {"hot_routes": float(np.mean([d["hot"] for d in rs])), "cold_routes": float(np.mean([d["n_cold"] for d in rs])),
+             "cold_experts": n_cold, "cold_experts_union": len(union),
+             "cold_union_MB": round(len(union) * exp_bytes / 1e6, 1),
              "gpu_ms": round(gpu_ms, 4), "cpu_ms": round(cpu_ms, 4), "hybrid_ms": round(hy_ms, 4),
+             "handoff_ms": round(hy_ms - cpu_ms, 4),
              "cpu_GBps": round(n_cold * exp_bytes / (cpu_ms * 1e-3) / 1e9, 1),
              "overlap": round((gpu_ms + cpu_ms - hy_ms) / max(min(gpu_ms, cpu_ms), 1e-9), 3)}
         res[f"T{T}"] = r

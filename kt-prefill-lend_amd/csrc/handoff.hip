@@ -8,12 +8,15 @@
 // submit's sequence number in pinned memory once all its blocks' writes are visible; the
 // engine's worker thread spins on that number (an event on the stream is the fallback),
 // runs the cold routes on the host cores (cpu_moe.cpp) into a pinned bf16 output.
-// The stream goes on with the GPU's hot experts meanwhile. sync_add(out): the host spins
-// until the worker is done, then out = bf16(out + cpu) on the stream (the wrapper's
-// `output + cpu_output`), the add kernel reading the CPU output from pinned memory through
-// its device address (no separate copy). The pinned output is written again only after
-// that add has completed (event out_free), so back-to-back layers cannot overwrite it
-// early. One submit is outstanding at a time per engine.
+// The stream goes on with the GPU's hot experts meanwhile. sync_add(out): out = bf16(out +
+// cpu) on the stream (the wrapper's `output + cpu_output`), the add kernel reading the CPU
+// output from pinned memory through its device address (no separate copy), and the host
+// spins until the worker is done, as sync_forward blocks. For decode windows the add is
+// enqueued before that wait and starts on a completion word the worker stores in pinned
+// memory, so no launch sits between the CPU side's end and the add; larger layers launch
+// their add after the wait. The pinned output is written again only after that add has
+// completed (event out_free), so back-to-back layers cannot overwrite it early. One submit
+// is outstanding at a time per engine.
 #include <algorithm>
 #include <atomic>
 #include <chrono>
@@ -23,6 +26,12 @@
 
 #include "cpu_moe.h"
 #include "kernels.h"
+
+// sync_add enqueues its add ahead of the CPU side's end for layers of at most this many
+// tokens (decode windows, whose CPU side takes milliseconds); that add waits at most
+// KTMI_WAIT_ADD_SECONDS for the CPU side. Larger layers are added once the CPU side is done.
+constexpr int64_t KTMI_WAIT_ADD_MAX_TOKENS = 256;
+constexpr uint64_t KTMI_WAIT_ADD_SECONDS = 10;
 
 struct ktmi_cpu_moe {
   ktmi_cpu::Engine* eng = nullptr;
@@ -43,8 +52,18 @@ struct ktmi_cpu_moe {
   uint32_t* seq_hd = nullptr;
   uint32_t* blocks_d = nullptr;
   uint32_t seq = 0;
-  hipEvent_t in_ready = nullptr, out_free = nullptr;
-  bool out_free_pending = false;
+  // completion words the worker publishes in pinned memory (device address fin_hd) for the
+  // add kernel sync_add enqueues ahead of the CPU side's end: [0] the last finished submit's
+  // sequence number, [1] the last successful one, [2] the last one whose add stopped waiting
+  uint32_t* fin_h = nullptr;
+  uint32_t* fin_hd = nullptr;
+  uint64_t wait_ticks = 0;  // that add's wait bound, in wall-clock ticks
+  hipEvent_t in_ready = nullptr;
+  // out_free[s & 1]: submit s's add is done with the pinned output. Two, so that sync_add of
+  // submit s, which may enqueue its add before the worker has started on s, never re-records
+  // the event the worker of s waits on (that of submit s - 1).
+  hipEvent_t out_free[2] = {nullptr, nullptr};
+  bool out_free_pending[2] = {false, false};
   std::thread worker;
   std::mutex m;
   std::condition_variable cv;
@@ -56,6 +75,10 @@ struct ktmi_cpu_moe {
 };
 
 namespace {
+
+using ktmi::bf2f;
+using ktmi::f2bf;
+using ktmi::f2bf2;
 
 // x [T, K] bf16 (16-byte chunks), ids and weights [P] into pinned host memory; then the
 // last block to finish publishes `seq` in pinned memory: every block makes its writes
@@ -82,6 +105,48 @@ __global__ __launch_bounds__(256) void stage_kernel(const u32x4_t* __restrict__ 
       *blocks_done = 0;
       __hip_atomic_store(seq_out, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
     }
+  }
+}
+
+// out += the CPU output of submit `seq` (add_bf16_kernel's arithmetic), enqueued before the
+// CPU side has finished: thread 0 of each block spins on the completion word fin[0] (system
+// scope, up to `limit` wall-clock ticks), then the block adds its 8 values a thread. A
+// forward that failed (fin[1] != seq) leaves out as it is; a wait past the bound writes NaN
+// and records seq in fin[2] for sync_add to report.
+__global__ __launch_bounds__(256) void wait_add_kernel(uint16_t* __restrict__ acc, const uint16_t* __restrict__ x,
+                                                        int64_t n, uint32_t* fin, uint32_t seq, uint64_t limit) {
+  __shared__ int go;
+  if (threadIdx.x == 0) {
+    const uint64_t t0 = (uint64_t)wall_clock64();
+    int st = 0;  // 0: timed out, 1: add, 2: the forward failed
+    for (;;) {
+      if ((int32_t)(__hip_atomic_load(fin, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) - seq) >= 0) {
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
+        st = __hip_atomic_load(fin + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) == seq ? 1 : 2;
+        break;
+      }
+      if ((uint64_t)wall_clock64() - t0 > limit) break;
+      __builtin_amdgcn_s_sleep(4);
+    }
+    if (st == 0) __hip_atomic_store(fin + 2, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    go = st;
+  }
+  __syncthreads();
+  if (go == 2) return;
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (i + 8 <= n) {
+    u32x4_t a = *(const u32x4_t*)(acc + i);
+    if (go == 1) {
+      const u32x4_t b = *(const u32x4_t*)(x + i);
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        a[k] = f2bf2(bf2f(a[k] & 0xFFFF) + bf2f(b[k] & 0xFFFF), bf2f(a[k] >> 16) + bf2f(b[k] >> 16));
+    } else {
+      a = u32x4_t{0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u};
+    }
+    *(u32x4_t*)(acc + i) = a;
+  } else {
+    for (int64_t j = i; j < n; ++j) acc[j] = go == 1 ? f2bf(bf2f(acc[j]) + bf2f(x[j])) : (uint16_t)0x7FC0;
   }
 }
 
@@ -131,9 +196,13 @@ void worker_loop(ktmi_cpu_moe* h) {
     wait_for(h, [h] { return h->stop || h->state.load() == ktmi_cpu_moe::SUBMITTED; }, 50);
     if (h->stop) return;
     int rc = staged_wait(h, h->seq, 2000);
-    if (rc == 0 && h->out_free_pending) rc = event_wait(h->out_free);
+    const int prev = (h->seq - 1) & 1;  // the previous submit's add must be done with out_h
+    if (rc == 0 && h->out_free_pending[prev]) rc = event_wait(h->out_free[prev]);
     if (rc == 0) rc = ktmi_cpu::engine_forward(h->eng, h->T, h->k, h->ids_h, h->w_h, h->x_h, h->out_h);
     h->rc = rc;
+    // the output's stores before the completion words (an add kernel may be waiting on them)
+    if (rc == 0) __atomic_store_n(h->fin_h + 1, h->seq, __ATOMIC_RELEASE);
+    __atomic_store_n(h->fin_h, h->seq, __ATOMIC_RELEASE);
     {
       std::lock_guard<std::mutex> g(h->m);
       h->state.store(ktmi_cpu_moe::DONE);
@@ -154,9 +223,12 @@ void destroy(ktmi_cpu_moe* h) {
   }
   if (h->in_ready || h->x_h) (void)hipSetDevice(h->device);
   // the last sync_add's add kernel may still be reading the pinned output
-  if (h->out_free_pending) (void)hipEventSynchronize(h->out_free);
+  for (int i = 0; i < 2; ++i)
+    if (h->out_free_pending[i]) (void)hipEventSynchronize(h->out_free[i]);
   if (h->in_ready) (void)hipEventDestroy(h->in_ready);
-  if (h->out_free) (void)hipEventDestroy(h->out_free);
+  for (int i = 0; i < 2; ++i)
+    if (h->out_free[i]) (void)hipEventDestroy(h->out_free[i]);
+  if (h->fin_h) (void)hipHostFree(h->fin_h);
   if (h->x_h) (void)hipHostFree(h->x_h);
   if (h->ids_h) (void)hipHostFree(h->ids_h);
   if (h->w_h) (void)hipHostFree(h->w_h);
@@ -210,7 +282,8 @@ ktmi_cpu_moe* ktmi_cpu_moe_create(int64_t hidden, int64_t inter, int type13, int
     if (e == hipSuccess) e = hipHostMalloc((void**)&h->w_h, P * 4, hipHostMallocDefault);
     if (e == hipSuccess) e = hipHostMalloc((void**)&h->out_h, (size_t)(max_tokens * hidden) * 2, hipHostMallocDefault);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&h->in_ready, hipEventDisableTiming);
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&h->out_free, hipEventDisableTiming);
+    for (int i = 0; i < 2; ++i)
+      if (e == hipSuccess) e = hipEventCreateWithFlags(&h->out_free[i], hipEventDisableTiming);
     if (e == hipSuccess) e = hipHostGetDevicePointer((void**)&h->x_hd, h->x_h, 0);
     if (e == hipSuccess) e = hipHostGetDevicePointer((void**)&h->ids_hd, h->ids_h, 0);
     if (e == hipSuccess) e = hipHostGetDevicePointer((void**)&h->w_hd, h->w_h, 0);
@@ -219,8 +292,16 @@ ktmi_cpu_moe* ktmi_cpu_moe_create(int64_t hidden, int64_t inter, int type13, int
     if (e == hipSuccess) e = hipHostGetDevicePointer((void**)&h->seq_hd, h->seq_h, 0);
     if (e == hipSuccess) e = hipMalloc((void**)&h->blocks_d, 4);
     if (e == hipSuccess) e = hipMemset(h->blocks_d, 0, 4);
+    if (e == hipSuccess) e = hipHostMalloc((void**)&h->fin_h, 64, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipHostGetDevicePointer((void**)&h->fin_hd, h->fin_h, 0);
+    int khz = 0;
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, h->device);
+    h->wait_ticks = (uint64_t)(khz > 0 ? khz : 100000) * 1000ull * KTMI_WAIT_ADD_SECONDS;
     if (e == hipSuccess) e = hipDeviceSynchronize();
-    if (e == hipSuccess) __atomic_store_n(h->seq_h, 0u, __ATOMIC_RELEASE);
+    if (e == hipSuccess) {
+      __atomic_store_n(h->seq_h, 0u, __ATOMIC_RELEASE);
+      for (int i = 0; i < 3; ++i) __atomic_store_n(h->fin_h + i, 0u, __ATOMIC_RELEASE);
+    }
   }
   if (e != hipSuccess) {
     set_error("cpu_moe_create: %s", hipGetErrorString(e));
@@ -296,6 +377,23 @@ int ktmi_cpu_moe_sync_add(ktmi_cpu_moe* h, void* out_bf16, void* stream) {
   clear_error();
   KTMI_REQUIRE(h, KTMI_EINVAL, "cpu_moe_sync_add: null engine");
   KTMI_REQUIRE(h->state.load() != ktmi_cpu_moe::IDLE, KTMI_EINVAL, "cpu_moe_sync_add: nothing submitted");
+  const int64_t T = h->T;
+  const uint32_t seq = h->seq;
+  const bool out_ok = out_bf16 && ((uintptr_t)out_bf16 % 16) == 0;
+  // the add reads the CPU result straight from pinned memory (no copy to the device first);
+  // out_free[seq & 1] marks when it is done, before the worker may write the next result
+  // there. A decode window's add goes on the stream now and waits there for the worker's
+  // completion word.
+  const bool ahead = T > 0 && T <= KTMI_WAIT_ADD_MAX_TOKENS && out_ok;
+  hipError_t early = hipSuccess;
+  if (ahead) {
+    const int64_t n = T * h->K;
+    wait_add_kernel<<<(unsigned)(((n + 7) / 8 + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+        (uint16_t*)out_bf16, h->out_hd, n, h->fin_hd, seq, h->wait_ticks);
+    early = hipGetLastError();
+    if (early == hipSuccess) early = hipEventRecord(h->out_free[seq & 1], (hipStream_t)stream);
+    if (early == hipSuccess) h->out_free_pending[seq & 1] = true;
+  }
   // the caller has nothing else to do here: spin through the CPU side's whole duration
   // (a decode layer's is well under this) rather than pay a wake-up on top of it
   wait_for(h, [h] { return h->state.load() == ktmi_cpu_moe::DONE; }, 2000);
@@ -303,16 +401,20 @@ int ktmi_cpu_moe_sync_add(ktmi_cpu_moe* h, void* out_bf16, void* stream) {
     std::lock_guard<std::mutex> g(h->m);
     h->state.store(ktmi_cpu_moe::IDLE);
   }
+  KTMI_HIP_TRY(early);
   KTMI_REQUIRE(h->rc == 0, KTMI_EHIP, "cpu_moe_sync_add: the CPU side failed (%d)", h->rc);
-  const int64_t T = h->T;
   if (T == 0) return KTMI_OK;
-  KTMI_REQUIRE(out_bf16 && ((uintptr_t)out_bf16 % 16) == 0, KTMI_EINVAL, "cpu_moe_sync_add: output null or not 16-byte aligned");
-  // the add reads the CPU result straight from pinned memory (no copy to the device first);
-  // out_free marks when it is done, before the worker may write the next result there
+  KTMI_REQUIRE(out_ok, KTMI_EINVAL, "cpu_moe_sync_add: output null or not 16-byte aligned");
+  if (ahead) {
+    KTMI_REQUIRE(__atomic_load_n(h->fin_h + 2, __ATOMIC_ACQUIRE) != seq, KTMI_EHIP,
+                 "cpu_moe_sync_add: the add stopped waiting for the CPU side after %llu s",
+                 (unsigned long long)KTMI_WAIT_ADD_SECONDS);
+    return KTMI_OK;
+  }
   const int rc = ktmi_add_bf16(out_bf16, h->out_hd, T * h->K, stream);
   if (rc) return rc;
-  KTMI_HIP_TRY(hipEventRecord(h->out_free, (hipStream_t)stream));
-  h->out_free_pending = true;
+  KTMI_HIP_TRY(hipEventRecord(h->out_free[seq & 1], (hipStream_t)stream));
+  h->out_free_pending[seq & 1] = true;
   return KTMI_OK;
 }
 

@@ -31,7 +31,7 @@ def _setup(dev):
     bank = [torch.from_numpy(np.ascontiguousarray(w13[:, :N].reshape(E, -1))).pin_memory(),
             torch.from_numpy(np.ascontiguousarray(w13[:, N:].reshape(E, -1))).pin_memory(),
             torch.from_numpy(np.ascontiguousarray(w2.reshape(E, -1))).pin_memory()]
-    cpu = CM.KTCPUExperts(*bank, K, N, TYPES, threads=8, max_tokens=128, max_top_k=TOPK)
+    cpu = CM.KTCPUExperts(*bank, K, N, TYPES, threads=8, max_tokens=320, max_top_k=TOPK)
     W13, W2 = to_dev(w13[:S], dev), to_dev(w2[:S], dev)  # logical experts 0..S-1 resident
     desc = H.layer_desc(W13, W2, K, N, TYPES[0], TYPES[2])
     return w13, w2, cpu, (W13, W2, desc)
@@ -52,7 +52,9 @@ def test_hybrid_layer(dev):
 
     w13, w2, cpu, (W13, W2, desc) = _setup(dev)
     g, d = dequant_w(w13, w2, TYPES, K, N)
-    for rep, T in enumerate((40, 3, 0, 96)):  # back-to-back layers, an empty one
+    # back-to-back layers, an empty one; up to 256 tokens sync_add enqueues its add before the
+    # CPU side ends (it waits on the worker's completion word), the 300-token layer adds after
+    for rep, T in enumerate((40, 3, 0, 300, 96, 1)):
         ids, w = _routes(T, 20 + rep)
         slot = np.where(ids < S, ids, -1).astype(np.int32)
         cold = np.where(ids < S, -1, ids).astype(np.int32)
