@@ -354,13 +354,9 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
     a_rd[s] = (wm * FJ * 32 + l32) * A_ROW + 16 * lds_slot(l32, q);
   }
 
+  // the accumulators start at the tile's first MFMAs, whose C operand is the constant 0
+  // (the first step is peeled off the K loop): no separate zeroing of 256 AGPRs a lane
   f32x16_t acc[FI][FJ];
-#pragma unroll
-  for (int i = 0; i < FI; ++i)
-#pragma unroll
-    for (int j = 0; j < FJ; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
   // raw ring: slot (k & 1) holds the bytes of step k (loaded two steps ahead); wv[k & 1]
   // the decoded weights of step k (decoded one step ahead)
@@ -403,8 +399,9 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
   for (int i = 0; i < FI; ++i) BP::template decode<0>(head[i], raw[0][i], grid_lds, wv[0][i]);
 
   int abuf = 0;
-  auto step = [&](int sb, auto subc) {
+  auto step = [&](int sb, auto subc, auto firstc) {
     constexpr int SUB = decltype(subc)::value;
+    constexpr bool FIRST = decltype(firstc)::value;  // the tile's first step: C starts at 0
     constexpr int cur = SUB & 1;
     constexpr int SUB1 = (SUB + 1) & 3, SUB2 = (SUB + 2) & 3, SUB3 = (SUB + 3) & 3;
     const int sb2 = SUB < 2 ? sb : min(sb + 1, lsb);
@@ -447,7 +444,8 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
         for (int j = 0; j < FJ; ++j)
 #pragma unroll
           for (int i = 0; i < FI; ++i)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[i], af[t][j], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                wf[i], af[t][j], FIRST && s == 0 ? f32x16_t{} : acc[i][j], 0, 0, 0);
         if (t == 0 && s2 == 0) {
 #pragma unroll
           for (int j = 0; j < FJ; ++j) af[0][j] = *(const bf16x8_t*)(Ab + j * 32 * A_ROW + a_rd[2]);
@@ -536,11 +534,17 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
     }
   };
 
-  for (int sb = 0; sb < nsb; ++sb) {
-    step(sb, S0{});
-    step(sb, S1{});
-    step(sb, S2{});
-    step(sb, S3{});
+  using ON = std::true_type;
+  using OFF = std::false_type;
+  step(0, S0{}, ON{});  // nsb >= 1: the layer requires Kdim to be a multiple of 256
+  step(0, S1{}, OFF{});
+  step(0, S2{}, OFF{});
+  step(0, S3{}, OFF{});
+  for (int sb = 1; sb < nsb; ++sb) {
+    step(sb, S0{}, OFF{});
+    step(sb, S1{}, OFF{});
+    step(sb, S2{}, OFF{});
+    step(sb, S3{}, OFF{});
   }
   if constexpr (!GATEUP) {
     flush();

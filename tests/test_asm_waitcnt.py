@@ -10,8 +10,9 @@ sources for gfx950 and count the instructions actually emitted.
   k the activation tile of step k+1, whose direct buffer->LDS loads were issued during step
   k-2, must have landed, so the step-end wait's n must not exceed the vector-memory
   instructions issued after that tile's last direct load (cyclically over the 4 steps of the
-  unrolled super-block loop, and from the prologue into the first step); the prologue's own
-  wait for tile 0 likewise; and no vmcnt(0) may drain the prefetch inside the K loop.
+  unrolled super-block loop, and in issue order over the first super-block, which is peeled
+  off the loop, and the loop's first iteration); the prologue's own wait for tile 0
+  likewise; and no vmcnt(0) may drain the prefetch inside the K loop.
 """
 import os
 import re
@@ -102,16 +103,32 @@ def test_grouped_gemm_counted_waits_cover_the_activation_tiles(tmp_path):
             after += sum(1 for j in steps[(s - 1) % 4] if VMEM.match(body[j]))
             after += sum(1 for j in steps[s] if VMEM.match(body[j]))
             assert 0 < waits[s] <= after, (name, "step", s, waits[s], after)
-        # the prologue: 3 tiles of AJ direct loads, then the wait for tile 0 and a barrier
-        pro = lines[st:a]
+        # before the loop: the prologue (3 tiles of AJ direct loads, then the wait for tile 0
+        # and a barrier) and the first super-block's 4 steps, peeled off the loop (their
+        # first MFMAs start the accumulators at 0)
+        pre = lines[st:a]
+        pbars = [j for j, l in enumerate(pre) if l.strip() == "s_barrier"]
+        assert len(pbars) == 5, (name, "the prologue's barrier + 4 peeled steps", len(pbars))
+        bar0 = pbars[0]
+        pro = pre[:bar0]
         dmas = [j for j, l in enumerate(pro) if DMA.match(l)]
         assert len(dmas) % 3 == 0 and dmas, (name, len(dmas))
         aj = len(dmas) // 3
-        bar0 = next(j for j in range(dmas[-1], len(pro)) if pro[j].strip() == "s_barrier")
         w0 = next(pro[j] for j in reversed(range(dmas[-1], bar0)) if "s_waitcnt" in pro[j] and "vmcnt" in pro[j])
-        after0 = sum(1 for l in pro[dmas[aj - 1] + 1:bar0] if VMEM.match(l))
+        after0 = sum(1 for l in pro[dmas[aj - 1] + 1:] if VMEM.match(l))
         assert 0 < _vmcnt(w0) <= after0, (name, "prologue", _vmcnt(w0), after0)
-        # entry into step 0: tile 1 = the prologue's direct loads aj .. 2 aj - 1
-        after1 = sum(1 for l in pro[dmas[2 * aj - 1] + 1:] if VMEM.match(l))
-        after1 += sum(1 for j in steps[0] if j >= 0 and VMEM.match(body[j]) and j < bars[0])
-        assert waits[0] <= after1, (name, "entry", waits[0], after1)
+        # the first 8 steps as issued: the 4 peeled ones, then the loop's first iteration;
+        # step k's closing wait needs tile k + 1, loaded by the prologue (k < 2) or by step
+        # k - 2: at least that many VMEM ops must follow the tile's last direct load
+        seq = [pre[pbars[s] + 1:pbars[s + 1]] for s in range(4)] + [[body[j] for j in steps[s]] for s in range(4)]
+        for k in range(8):
+            w = next(l for l in reversed(seq[k]) if "s_waitcnt" in l and "vmcnt" in l)
+            if k < 2:
+                after = sum(1 for l in pro[dmas[(k + 2) * aj - 1] + 1:] if VMEM.match(l))
+            else:
+                src = seq[k - 2]
+                last = max(p for p, l in enumerate(src) if DMA.match(l))
+                after = sum(1 for l in src[last + 1:] if VMEM.match(l))
+            after += sum(1 for q in range(max(k - 1, 0), k + 1) for l in seq[q] if VMEM.match(l)) if k >= 2 else \
+                sum(1 for q in range(0, k + 1) for l in seq[q] if VMEM.match(l))
+            assert 0 < _vmcnt(w) <= after, (name, "step", k, _vmcnt(w), after)
