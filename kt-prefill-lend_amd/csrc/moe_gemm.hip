@@ -260,7 +260,7 @@ __global__ __launch_bounds__(NTHREADS, (gemm_waves_per_simd<TYPE, FJ>()))
 void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const int32_t* __restrict__ perm,
                   const int4* __restrict__ tile_info, int top_k, const uint8_t* __restrict__ W, int w_is_table,
                   int64_t w_expert_stride, int64_t rb, int Kdim, int NI, int NT, int64_t nblk,
-                  uint16_t* __restrict__ out) {
+                  uint16_t* __restrict__ out, uint32_t out_bytes) {
   constexpr int BM = tile_m<FJ>();
   constexpr int A_BYTES = BM * A_ROW;
   constexpr int AJ = A_BYTES / (16 * NTHREADS);  // direct loads per thread per step
@@ -520,16 +520,18 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
         }
       }
       __syncthreads();
-      const int64_t col0 = (int64_t)nt * CCOLS;
+      // buffer stores with 32-bit offsets (out_bytes < 4 GiB), no branch: a row past the
+      // tile's routes (orow -1) gets an offset past the buffer, and the store is dropped
+      const __amdgpu_buffer_rsrc_t y_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)out, (short)0, out_bytes, 0x00020000);
+      const uint32_t col_b = 2u * (uint32_t)(nt * CCOLS);
 #pragma unroll
       for (int it = 0; it < NIT; ++it) {
         const int qq = tid + it * NTHREADS;
         const int ml = qq / CW, c = qq % CW;
         const int orow = orow_lds[ml];
-        if (orow >= 0) {
-          const u32x4_t v = *(const u32x4_t*)(cs + ml * (CW * 16) + 16 * (c ^ (ml % CW)));
-          __builtin_nontemporal_store(v, (u32x4_t*)(out + (int64_t)orow * NI + col0 + 8 * c));
-        }
+        const u32x4_t v = *(const u32x4_t*)(cs + ml * (CW * 16) + 16 * (c ^ (ml % CW)));
+        const uint32_t off = orow >= 0 ? (uint32_t)orow * (2u * (uint32_t)NI) + col_b + 16u * (uint32_t)c : 0xFFFFFFF0u;
+        __builtin_amdgcn_raw_buffer_store_b128(v, y_rsrc, (int)off, 0, 2);  // nt: Y is read once, much later
       }
     }
   };
@@ -570,15 +572,17 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
       }
   }
   __syncthreads();
-  const int64_t col0 = (int64_t)nt * CCOLS;
+  // buffer stores with 32-bit offsets, no branch: rows past the tile's routes get an offset
+  // past the buffer and are dropped; cached (the down GEMM reads H back soon)
+  const __amdgpu_buffer_rsrc_t h_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)out, (short)0, out_bytes, 0x00020000);
+  const uint32_t col_b = 2u * (uint32_t)(nt * CCOLS);
 #pragma unroll
   for (int it = 0; it < NIT; ++it) {
     const int q = tid + it * NTHREADS;
     const int ml = q / CW, c = q % CW;
-    if (ml < valid) {
-      const u32x4_t v = *(const u32x4_t*)(cs + ml * (CW * 16) + 16 * (c ^ (ml % CW)));
-      *(u32x4_t*)(out + (int64_t)(m0 + ml) * NI + col0 + 8 * c) = v;  // read back by the down GEMM
-    }
+    const u32x4_t v = *(const u32x4_t*)(cs + ml * (CW * 16) + 16 * (c ^ (ml % CW)));
+    const uint32_t off = ml < valid ? (uint32_t)(m0 + ml) * (2u * (uint32_t)NI) + col_b + 16u * (uint32_t)c : 0xFFFFFFF0u;
+    __builtin_amdgcn_raw_buffer_store_b128(v, h_rsrc, (int)off, 0, 0);
   }
 }
 
@@ -614,33 +618,35 @@ __global__ __launch_bounds__(256) void combine_routes(const uint16_t* __restrict
 template <int TYPE, bool GATEUP, int FJ>
 void launch_gemm(dim3 grid, hipStream_t stream, const uint16_t* A_src, uint32_t a_bytes, const int32_t* perm,
                  const int4* tile_info, int top_k, const void* W, int w_is_table, int64_t w_expert_stride, int64_t rb,
-                 int Kdim, int NI, int NT, int64_t nblk, uint16_t* out) {
+                 int Kdim, int NI, int NT, int64_t nblk, uint16_t* out, uint32_t out_bytes) {
   grouped_gemm<TYPE, GATEUP, FJ><<<grid, NTHREADS, 0, stream>>>(A_src, a_bytes, perm, tile_info, top_k,
                                                                (const uint8_t*)W, w_is_table, w_expert_stride, rb,
-                                                               Kdim, NI, NT, nblk, out);
+                                                               Kdim, NI, NT, nblk, out, out_bytes);
 }
 
 template <bool GATEUP, int TYPE>
 void launch_fj(int fj, dim3 grid, hipStream_t stream, const uint16_t* A_src, uint32_t a_bytes,
                const int32_t* perm, const int4* tile_info, int top_k, const void* W, int w_is_table,
-               int64_t w_expert_stride, int64_t rb, int Kdim, int NI, int NT, int64_t nblk, uint16_t* out) {
+               int64_t w_expert_stride, int64_t rb, int Kdim, int NI, int NT, int64_t nblk, uint16_t* out,
+               uint32_t out_bytes) {
   if (fj == 8)
     launch_gemm<TYPE, GATEUP, 8>(grid, stream, A_src, a_bytes, perm, tile_info, top_k, W, w_is_table,
-                                 w_expert_stride, rb, Kdim, NI, NT, nblk, out);
+                                 w_expert_stride, rb, Kdim, NI, NT, nblk, out, out_bytes);
   else
     launch_gemm<TYPE, GATEUP, 4>(grid, stream, A_src, a_bytes, perm, tile_info, top_k, W, w_is_table,
-                                 w_expert_stride, rb, Kdim, NI, NT, nblk, out);
+                                 w_expert_stride, rb, Kdim, NI, NT, nblk, out, out_bytes);
 }
 
 template <bool GATEUP>
 int dispatch_gemm(int type, int fj, dim3 grid, hipStream_t stream, const uint16_t* A_src, uint32_t a_bytes,
                   const int32_t* perm, const int4* tile_info, int top_k, const void* W, int w_is_table,
-                  int64_t w_expert_stride, int64_t rb, int Kdim, int NI, int NT, int64_t nblk, uint16_t* out) {
+                  int64_t w_expert_stride, int64_t rb, int Kdim, int NI, int NT, int64_t nblk, uint16_t* out,
+                  uint32_t out_bytes) {
   switch (type) {
-    case GGML_Q8_0: launch_fj<GATEUP, GGML_Q8_0>(fj, grid, stream, A_src, a_bytes, perm, tile_info, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
-    case GGML_Q4_K: launch_fj<GATEUP, GGML_Q4_K>(fj, grid, stream, A_src, a_bytes, perm, tile_info, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
-    case GGML_Q6_K: launch_fj<GATEUP, GGML_Q6_K>(fj, grid, stream, A_src, a_bytes, perm, tile_info, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
-    case GGML_IQ3_S: launch_fj<GATEUP, GGML_IQ3_S>(fj, grid, stream, A_src, a_bytes, perm, tile_info, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out); break;
+    case GGML_Q8_0: launch_fj<GATEUP, GGML_Q8_0>(fj, grid, stream, A_src, a_bytes, perm, tile_info, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out, out_bytes); break;
+    case GGML_Q4_K: launch_fj<GATEUP, GGML_Q4_K>(fj, grid, stream, A_src, a_bytes, perm, tile_info, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out, out_bytes); break;
+    case GGML_Q6_K: launch_fj<GATEUP, GGML_Q6_K>(fj, grid, stream, A_src, a_bytes, perm, tile_info, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out, out_bytes); break;
+    case GGML_IQ3_S: launch_fj<GATEUP, GGML_IQ3_S>(fj, grid, stream, A_src, a_bytes, perm, tile_info, top_k, W, w_is_table, w_expert_stride, rb, Kdim, NI, NT, nblk, out, out_bytes); break;
     default: set_error("grouped GEMM: ggml type %d has no kernel", type); return KTMI_ETYPE;
   }
   KTMI_HIP_TRY(hipGetLastError());
@@ -692,7 +698,8 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
                (long long)K, BNW > 256 ? BNW : 256);
   KTMI_REQUIRE(N % (BNW / 2) == 0 && N % 256 == 0, KTMI_EINVAL,
                "grouped layer: intermediate %lld not a multiple of 256", (long long)N);
-  KTMI_REQUIRE(tokens * K * 2 <= 0xFFFFFFFFll && R * N * 2 <= 0xFFFFFFFFll, KTMI_EINVAL,
+  // x, H and Y are addressed by buffer instructions with 32-bit offsets
+  KTMI_REQUIRE(tokens * K * 2 <= 0xFFFFFFFFll && R * N * 2 <= 0xFFFFFFFFll && R * K * 2 <= 0xFFFFFFFFll, KTMI_EINVAL,
                "grouped layer: activations of %lld tokens exceed the 4 GiB buffer range", (long long)tokens);
   if (tokens == 0) return KTMI_OK;
   int32_t* hist = (int32_t*)(ws + P.off_counts);
@@ -718,7 +725,8 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
   const int64_t nblk1 = P.max_tiles * NT1;
   dim3 g1((unsigned)((nblk1 + 8 * NT1 - 1) / (8 * NT1) * (8 * NT1)));
   int rc = dispatch_gemm<true>(L->type13, P.fj, g1, stream, x, (uint32_t)(tokens * K * 2), perm, tile_info,
-                               (int)top_k, L->w13, L->w_is_table, st13, rb13, (int)K, (int)N, NT1, nblk1, H);
+                               (int)top_k, L->w13, L->w_is_table, st13, rb13, (int)K, (int)N, NT1, nblk1, H,
+                               (uint32_t)(R * N * 2));
   if (rc) return rc;
   record_stage(2, stream);  // no mid stage on this path: SiLU*mul is in the gate/up epilogue
   record_stage(3, stream);
@@ -726,7 +734,7 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
   const int64_t nblk2 = P.max_tiles * NT2;
   dim3 g2((unsigned)((nblk2 + 8 * NT2 - 1) / (8 * NT2) * (8 * NT2)));
   rc = dispatch_gemm<false>(L->type2, P.fj, g2, stream, H, (uint32_t)(R * N * 2), perm, tile_info, (int)top_k,
-                            L->w2, L->w_is_table, st2, rb2, (int)N, (int)K, NT2, nblk2, Y);
+                            L->w2, L->w_is_table, st2, rb2, (int)N, (int)K, NT2, nblk2, Y, (uint32_t)(R * K * 2));
   if (rc) return rc;
   record_stage(4, stream);
   for (int64_t t0 = 0; t0 < tokens; t0 += 65535) {
