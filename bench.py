@@ -11,8 +11,11 @@ legs: `configs` (Q8_0 512 tokens, 2K and 32K chunks, IQ3_S 16K against the MFMA 
 `decode` (1/4/8/16-token layers against HBM), `stream` (four large layers streamed from
 pinned host memory) and `hybrid` (hot routes on the GPU, cold ones on the host cores).
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-configs]
-                    [--no-decode] [--no-stream] [--no-hybrid]
+`sustained` repeats the headline measurement after 150 more untimed steps, once the GPU's
+clocks have settled under load.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--sustained 100] [--no-cpu]
+                    [--no-configs] [--no-decode] [--no-stream] [--no-hybrid]
 """
 from __future__ import annotations
 
@@ -86,9 +89,11 @@ def log(msg):
 
 def time_layer(P, torch, desc_list, x, w, slot, mode, steps, warmup, ev: HipEvents, breakdown_steps=None):
     """Warmup, then `steps` timed layer calls with events only around the loop (desc_list
-    rotates weight copies per step). Then `breakdown_steps` more calls with an event at every
-    stage boundary (each event adds a few microseconds of stream time, so the per-stage
-    means come from their own pass and do not inflate the step time).
+    rotates weight copies per step). Then, enqueued right behind them with no host wait in
+    between (the GPU's clocks keep rising over the first ~100 back-to-back steps, so a pause
+    or a later pass would see a different clock state), `breakdown_steps` more calls with an
+    event at every stage boundary (each event adds a few microseconds of stream time, so the
+    per-stage means come from their own pass and do not inflate the step time).
     Returns (ms per step, per-stage mean ms, output)."""
     H, L = P.kt_gguf_hot, P._lib
     lib = L.lib()
@@ -97,25 +102,24 @@ def time_layer(P, torch, desc_list, x, w, slot, mode, steps, warmup, ev: HipEven
     need = max(lib.ktmi_moe_layer_workspace(d, T, k, mode) for d in desc_list)
     ws = torch.empty((need,), dtype=torch.uint8, device=x.device)
     stream = L.stream_ptr(x.device)
+    nb = breakdown_steps or steps
+    se = ev.create(2)
+    stage_ev = ev.create(nb * L.STAGE_EVENTS)
     for i in range(warmup):
         H.moe_layer(desc_list[i % len(desc_list)], x, w, slot, mode, out, ws)
-    se = ev.create(2)
     torch.cuda.synchronize()
     ev.record(se[0], stream)
     for i in range(steps):
         H.moe_layer(desc_list[i % len(desc_list)], x, w, slot, mode, out, ws)
     ev.record(se[1], stream)
-    torch.cuda.synchronize()
-    total = ev.ms(se[0], se[1])
-    ev.destroy(se)
-    nb = breakdown_steps or steps
-    stage_ev = ev.create(nb * L.STAGE_EVENTS)
     for i in range(nb):
         arr = (C.c_void_p * L.STAGE_EVENTS)(*stage_ev[i * L.STAGE_EVENTS:(i + 1) * L.STAGE_EVENTS])
         L.check(lib.ktmi_set_stage_events(arr, L.STAGE_EVENTS))
         H.moe_layer(desc_list[i % len(desc_list)], x, w, slot, mode, out, ws)
     L.check(lib.ktmi_set_stage_events(None, 0))
     torch.cuda.synchronize()
+    total = ev.ms(se[0], se[1])
+    ev.destroy(se)
     per = np.zeros((nb, len(STAGES)))
     for i in range(nb):
         b = i * L.STAGE_EVENTS
@@ -138,6 +142,9 @@ def main():
                     help="skip the other workload shapes (Q8_0 512 tokens, 2K/32K chunks, IQ3_S 16K)")
     ap.add_argument("--no-hybrid", action="store_true", help="skip the GPU + CPU decode leg")
     ap.add_argument("--cpu-tokens", type=int, default=1024, help="tokens of the chunk timed on the CPU")
+    ap.add_argument("--sustained", type=int, default=100, metavar="K",
+                    help="after the headline, time K more layer steps behind 150 back-to-back untimed ones "
+                         "(the GPU's clocks settle under sustained load); 0 skips this leg")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run an fp32 negate of MIB MiB (reads and writes exactly MIB MiB), the known-size "
                          "kernel that scales FETCH_SIZE/WRITE_SIZE counters to bytes")
@@ -225,6 +232,21 @@ def main():
                      "stage_ms": {k: round(v, 4) for k, v in stages.items()}},
         "cpu_baseline": None,
     }
+
+    if args.sustained:
+        # the headline's few warmup steps leave the GPU in its clock ramp (a layer step runs
+        # ~0.88 ms from idle and settles near 0.68 ms after ~100 back-to-back steps); this leg
+        # reports the settled rate beside it, measured the same way
+        sw = 150
+        ms2, st2, _ = time_layer(P, torch, [desc], x, tw_d, slot_d, L.MODE_GROUPED, args.sustained, sw, ev)
+        result["sustained"] = {
+            "warmup": sw, "steps": args.sustained, "ms_per_step": round(ms2, 4),
+            "tokens_per_s": round(T / (ms2 * 1e-3), 1),
+            "layer_frac": round((flop_gu + flop_dn) / (ms2 * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "gate_up_frac": round(flop_gu / (st2["gate_up"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "down_frac": round(flop_dn / (st2["down"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "stage_ms": {k: round(v, 4) for k, v in st2.items()}}
+        log(f"sustained: {result['sustained']}")
 
     if not args.no_configs:
         result["configs"] = bench_configs(P, torch, S, ev, dev)
