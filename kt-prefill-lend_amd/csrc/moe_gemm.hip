@@ -270,7 +270,13 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
   // waits for all of them (vmcnt(0)) before every LDS read, which drains the prefetch.
   constexpr int GRID_BYTES = TYPE == GGML_IQ3_S ? 512 * 4 : 0;
   constexpr int OROW_BYTES = GATEUP ? 0 : BM * 4;  // down: the tile's output row indices
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[AD * A_BYTES + GRID_BYTES + OROW_BYTES];
+  // 256-route tiles (one block per CU, LDS to spare): each wave stages its own 32-route slices
+  // of the C tile, so the epilogue needs no workgroup barrier
+  constexpr bool WAVE_STG = FJ == 8;
+  constexpr int STG_COLS = GATEUP ? FI / 2 * 32 : FI * 32;  // the wave's output columns
+  constexpr int STG_WAVE = 32 * STG_COLS * 2;                // 32 routes of them, bf16
+  constexpr int STG_BYTES = WAVE_STG ? NWAVES * STG_WAVE : 0;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[AD * A_BYTES + GRID_BYTES + OROW_BYTES + STG_BYTES];
   uint32_t* const grid_lds = (uint32_t*)(smem + AD * A_BYTES);
   int32_t* const orow_lds = (int32_t*)(smem + AD * A_BYTES + GRID_BYTES);
   using BP = BPiece<TYPE>;
@@ -503,7 +509,39 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
   // down: the accumulators to the bf16 output rows Y[perm[m]] (streamed past the caches: Y is
   // read once, by the combine, long after)
   auto flush = [&]() {
-    if constexpr (!GATEUP) {
+    if constexpr (WAVE_STG && !GATEUP) {
+      // per 32-route slice j: the wave's 32 x FI*32 block into its staging area (rows of
+      // 128 B, chunk c of row r at slot c ^ (r % 8)), then 8 rows x 128 B per store. A
+      // wave's LDS operations complete in order, so no barrier sits between the writes and
+      // the reads of other lanes, nor between the reads and the next slice's writes.
+      __builtin_amdgcn_s_waitcnt(0);  // the clamped prefetches of the last steps (into LDS) have landed
+      uint8_t* stg = smem + AD * A_BYTES + GRID_BYTES + OROW_BYTES + wave * STG_WAVE;
+      const __amdgpu_buffer_rsrc_t y_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)out, (short)0, out_bytes, 0x00020000);
+      const uint32_t col_b = 2u * (uint32_t)(nt * CCOLS + wn * FI * 32) + 16u * (uint32_t)(lane & 7);
+#pragma unroll
+      for (int j = 0; j < FJ; ++j) {
+#pragma unroll
+        for (int i = 0; i < FI; ++i)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+            const f32x16_t& v = acc[i][j];
+            const u32x2_t w = {f2bf2(v[4 * r4], v[4 * r4 + 1]), f2bf2(v[4 * r4 + 2], v[4 * r4 + 3])};
+            *(u32x2_t*)(stg + l32 * 128 + 16 * ((4 * i + r4) ^ (l32 & 7)) + 8 * h) = w;
+          }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+          const int row = 8 * it + (lane >> 3);
+          const u32x4_t v = *(const u32x4_t*)(stg + row * 128 + 16 * ((lane & 7) ^ (row & 7)));
+          const int orow = orow_lds[32 * j + row];
+          const uint32_t off = orow >= 0 ? (uint32_t)orow * (2u * (uint32_t)NI) + col_b : 0xFFFFFFF0u;
+          __builtin_amdgcn_raw_buffer_store_b128(v, y_rsrc, (int)off, 0, 2);  // nt: Y is read once, much later
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+    } else if constexpr (!GATEUP) {
       __builtin_amdgcn_s_waitcnt(0);  // the clamped prefetches of the last steps (into LDS)
       __syncthreads();                 // every wave is done with the activation buffers
 #pragma unroll
@@ -552,11 +590,49 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
     flush();
     return;
   }
+  constexpr int FH = FI / 2;
+  if constexpr (WAVE_STG) {
+    // ---- gate/up epilogue, per wave: silu(gate) * up of each 32-route slice j into the
+    // wave's staging area (rows of 64 B, chunk c of row r at slot c ^ sw(r): any 8 or 16
+    // consecutive rows spread over the banks), then 16 rows x 64 B per store (the other
+    // waves write the rest of each H row segment)
+    static_assert(FH == 1, "one gate and one up fragment per wave");
+    __builtin_amdgcn_s_waitcnt(0);  // the clamped prefetches of the last steps (into LDS) have landed
+    uint8_t* stg = smem + AD * A_BYTES + GRID_BYTES + OROW_BYTES + wave * STG_WAVE;
+    auto sw = [](int r) { return ((r >> 1) ^ (r >> 3)) & 3; };
+    const __amdgpu_buffer_rsrc_t h_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)out, (short)0, out_bytes, 0x00020000);
+    const uint32_t col_b = 2u * (uint32_t)(nt * CCOLS + wn * 32) + 16u * (uint32_t)(lane & 3);
+#pragma unroll
+    for (int j = 0; j < FJ; ++j) {
+      const f32x16_t& g = acc[0][j];
+      const f32x16_t& u = acc[1][j];
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const u32x2_t v = {f2bf2(silu_mul(g[4 * r4], u[4 * r4]), silu_mul(g[4 * r4 + 1], u[4 * r4 + 1])),
+                           f2bf2(silu_mul(g[4 * r4 + 2], u[4 * r4 + 2]), silu_mul(g[4 * r4 + 3], u[4 * r4 + 3]))};
+        *(u32x2_t*)(stg + l32 * 64 + 16 * (r4 ^ sw(l32)) + 8 * h) = v;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int it = 0; it < 2; ++it) {
+        const int row = 16 * it + (lane >> 2);
+        const u32x4_t v = *(const u32x4_t*)(stg + row * 64 + 16 * ((lane & 3) ^ sw(row)));
+        const int ml = 32 * j + row;
+        // rows past the tile's routes get an offset past the buffer and are dropped; cached
+        // (the down GEMM reads H back soon)
+        const uint32_t off = ml < valid ? (uint32_t)(m0 + ml) * (2u * (uint32_t)NI) + col_b : 0xFFFFFFF0u;
+        __builtin_amdgcn_raw_buffer_store_b128(v, h_rsrc, (int)off, 0, 0);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    return;
+  }
   __builtin_amdgcn_s_waitcnt(0);  // the clamped prefetches of the last steps
   __syncthreads();                 // every wave is done with the activation buffers
 
   // ---- gate/up epilogue: silu(gate) * up into the C tile, then whole rows of H
-  constexpr int FH = FI / 2;
 #pragma unroll
   for (int j = 0; j < FJ; ++j) {
     const int ml = 32 * (wm * FJ + j) + l32;
