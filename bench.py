@@ -87,14 +87,17 @@ def log(msg):
     print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
 
 
-def time_layer(P, torch, desc_list, x, w, slot, mode, steps, warmup, ev: HipEvents, breakdown_steps=None):
-    """Warmup, then `steps` timed layer calls with events only around the loop (desc_list
-    rotates weight copies per step). Then, enqueued right behind them with no host wait in
-    between (the GPU's clocks keep rising over the first ~100 back-to-back steps, so a pause
-    or a later pass would see a different clock state), `breakdown_steps` more calls with an
-    event at every stage boundary (each event adds a few microseconds of stream time, so the
-    per-stage means come from their own pass and do not inflate the step time).
-    Returns (ms per step, per-stage mean ms, output)."""
+def time_layer(P, torch, desc_list, x, w, slot, mode, steps, warmup, ev: HipEvents, breakdown_steps=None,
+               sample_every=4):
+    """Warmup, then `steps` timed layer calls (desc_list rotates weight copies per step) with
+    events around the loop and, on every `sample_every`-th call, around its gate/up and down
+    GEMMs (4 events, about 1 us of stream time each, so the sampled kernel durations are those
+    of the timed steps themselves at a cost of about 1 us per step). Then, enqueued right
+    behind them with no host wait in between (the GPU's clocks keep rising over the first ~100
+    back-to-back steps, so a pause or a later pass would see a different clock state),
+    `breakdown_steps` more calls with an event at every stage boundary, for the per-stage means.
+    Returns (ms per step, per-stage mean ms of the breakdown calls, output, mean ms of the
+    gate/up and down GEMMs over the sampled timed calls)."""
     H, L = P.kt_gguf_hot, P._lib
     lib = L.lib()
     T, k = slot.shape
@@ -105,12 +108,22 @@ def time_layer(P, torch, desc_list, x, w, slot, mode, steps, warmup, ev: HipEven
     nb = breakdown_steps or steps
     se = ev.create(2)
     stage_ev = ev.create(nb * L.STAGE_EVENTS)
+    sampled = [i for i in range(steps) if i % sample_every == sample_every - 1] if sample_every else []
+    kev = ev.create(4 * len(sampled)) if sampled else []  # gate/up start, end, down start, end (boundaries 1-4)
     for i in range(warmup):
         H.moe_layer(desc_list[i % len(desc_list)], x, w, slot, mode, out, ws)
     torch.cuda.synchronize()
     ev.record(se[0], stream)
+    n = 0
     for i in range(steps):
-        H.moe_layer(desc_list[i % len(desc_list)], x, w, slot, mode, out, ws)
+        if n < len(sampled) and i == sampled[n]:
+            arr = (C.c_void_p * L.STAGE_EVENTS)(None, *kev[4 * n:4 * n + 4], None)
+            L.check(lib.ktmi_set_stage_events(arr, L.STAGE_EVENTS))
+            H.moe_layer(desc_list[i % len(desc_list)], x, w, slot, mode, out, ws)
+            L.check(lib.ktmi_set_stage_events(None, 0))
+            n += 1
+        else:
+            H.moe_layer(desc_list[i % len(desc_list)], x, w, slot, mode, out, ws)
     ev.record(se[1], stream)
     for i in range(nb):
         arr = (C.c_void_p * L.STAGE_EVENTS)(*stage_ev[i * L.STAGE_EVENTS:(i + 1) * L.STAGE_EVENTS])
@@ -126,7 +139,13 @@ def time_layer(P, torch, desc_list, x, w, slot, mode, steps, warmup, ev: HipEven
         for s in range(len(STAGES)):
             per[i, s] = ev.ms(stage_ev[b + s], stage_ev[b + s + 1])
     ev.destroy(stage_ev)
-    return total / steps, dict(zip(STAGES, per.mean(axis=0).tolist())), out
+    timed = None
+    if sampled:
+        timed = {"gate_up": float(np.mean([ev.ms(kev[4 * j], kev[4 * j + 1]) for j in range(len(sampled))])),
+                 "down": float(np.mean([ev.ms(kev[4 * j + 2], kev[4 * j + 3]) for j in range(len(sampled))])),
+                 "samples": len(sampled)}
+        ev.destroy(kev)
+    return total / steps, dict(zip(STAGES, per.mean(axis=0).tolist())), out, timed
 
 
 def main():
@@ -184,17 +203,19 @@ def main():
     W2 = torch.from_numpy(w2).to(dev)
     H, L = P.kt_gguf_hot, P._lib
     desc = H.layer_desc(W13, W2, w.hidden, w.inter, w.types[0], w.types[2])
-    ms, stages, out = time_layer(P, torch, [desc], x, tw_d, slot_d, L.MODE_GROUPED, args.steps, args.warmup, ev)
+    ms, stages, out, timed = time_layer(P, torch, [desc], x, tw_d, slot_d, L.MODE_GROUPED, args.steps, args.warmup, ev)
     r_hot = int((slot >= 0).sum())
     flop_gu = 4.0 * w.hidden * w.inter * r_hot
     flop_dn = 2.0 * w.hidden * w.inter * r_hot
-    kern = {"gate_up": (flop_gu, stages["gate_up"]), "down": (flop_dn, stages["down"])}
+    # the GEMMs' durations in the timed steps themselves (sampled every 4th step)
+    kern = {"gate_up": (flop_gu, timed["gate_up"]), "down": (flop_dn, timed["down"])}
     dom = max(kern, key=lambda k: kern[k][1])
     achieved = kern[dom][0] / (kern[dom][1] * 1e-3) / 1e12
     tok_s = T / (ms * 1e-3)
     layer_tflops = (flop_gu + flop_dn) / (ms * 1e-3) / 1e12
     log(f"layer {ms:.3f} ms/step, {tok_s / 1e6:.2f} M tok/s, {layer_tflops:.0f} TFLOP/s "
-        f"({100 * layer_tflops / PEAK_BF16_TFLOPS:.1f}% of bf16 peak); stages ms {stages}")
+        f"({100 * layer_tflops / PEAK_BF16_TFLOPS:.1f}% of bf16 peak); GEMMs in the timed steps ms {timed}; "
+        f"stages ms (breakdown pass) {stages}")
 
     def profiled(fname, field):
         # a figure of the dominant kernel from a committed rocprofv3 summary (None if absent)
@@ -229,6 +250,8 @@ def main():
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
                      "mfma_busy_counter": mfma_busy, "clock_GHz_counter": clock,
                      "layer_frac": round(layer_tflops / PEAK_BF16_TFLOPS, 4),
+                     "kernel_ms_timed": {"gate_up": round(timed["gate_up"], 4), "down": round(timed["down"], 4),
+                                         "samples": timed["samples"]},
                      "stage_ms": {k: round(v, 4) for k, v in stages.items()}},
         "cpu_baseline": None,
     }
@@ -238,13 +261,14 @@ def main():
         # ~0.88 ms from idle and settles near 0.68 ms after ~100 back-to-back steps); this leg
         # reports the settled rate beside it, measured the same way
         sw = 150
-        ms2, st2, _ = time_layer(P, torch, [desc], x, tw_d, slot_d, L.MODE_GROUPED, args.sustained, sw, ev)
+        ms2, st2, _, timed2 = time_layer(P, torch, [desc], x, tw_d, slot_d, L.MODE_GROUPED, args.sustained, sw, ev)
         result["sustained"] = {
             "warmup": sw, "steps": args.sustained, "ms_per_step": round(ms2, 4),
             "tokens_per_s": round(T / (ms2 * 1e-3), 1),
             "layer_frac": round((flop_gu + flop_dn) / (ms2 * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-            "gate_up_frac": round(flop_gu / (st2["gate_up"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-            "down_frac": round(flop_dn / (st2["down"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "gate_up_frac": round(flop_gu / (timed2["gate_up"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "down_frac": round(flop_dn / (timed2["down"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "kernel_ms_timed": {"gate_up": round(timed2["gate_up"], 4), "down": round(timed2["down"], 4)},
             "stage_ms": {k: round(v, 4) for k, v in st2.items()}}
         log(f"sustained: {result['sustained']}")
 
@@ -269,8 +293,8 @@ def main():
 def bench_configs(P, torch, S, ev, dev, steps=10, warmup=2):
     """The other prefill-sized workloads, one layer each in the mode the library picks: Q8_0
     at 512 tokens, the headline shapes at 2048 and 32768 tokens and IQ3_S at 16384. Reports
-    tokens/s and the gate/up and down GEMMs' TFLOP/s against the bf16 MFMA peak (stage
-    times from the event pass)."""
+    tokens/s and the gate/up and down GEMMs' TFLOP/s against the bf16 MFMA peak (their
+    durations sampled in the timed steps)."""
     H, L = P.kt_gguf_hot, P._lib
     lib = L.lib()
     cases = [("q8_0-h2048-n768-e128-k8-hot16", 512), (HEADLINE, 2048), (HEADLINE, 32768),
@@ -285,7 +309,9 @@ def bench_configs(P, torch, S, ev, dev, steps=10, warmup=2):
         W13, W2 = torch.from_numpy(w13).to(dev), torch.from_numpy(w2).to(dev)
         desc = H.layer_desc(W13, W2, w.hidden, w.inter, w.types[0], w.types[2])
         mode = lib.ktmi_moe_layer_mode(desc, T, w.top_k)
-        ms, stages, _ = time_layer(P, torch, [desc], x, tw_d, slot_d, mode, steps, warmup, ev)
+        ms, stages, _, timed = time_layer(P, torch, [desc], x, tw_d, slot_d, mode, steps, warmup, ev)
+        if timed:  # the GEMMs' durations in the timed steps
+            stages = dict(stages, gate_up=timed["gate_up"], down=timed["down"])
         r_hot = int((slot >= 0).sum())
         f_gu, f_dn = 4.0 * w.hidden * w.inter * r_hot, 2.0 * w.hidden * w.inter * r_hot
         rec = {"tokens": T, "mode": "grouped" if mode == L.MODE_GROUPED else "gemv", "hot_routes": r_hot,
@@ -332,7 +358,7 @@ def bench_decode(P, torch, S, ev, dev, steps=50, warmup=5, rotate_bytes=512e6):
         nbytes = uniq * exp_bytes + 2 * T * w.hidden * 2
         out = {}
         for name, dl in (("hbm", descs[:nc]), ("warm", descs[:1])):
-            ms, stages, _ = time_layer(P, torch, dl, x, tw_d, slot_d, L.MODE_GEMV, steps, warmup, ev)
+            ms, stages, _, _ = time_layer(P, torch, dl, x, tw_d, slot_d, L.MODE_GEMV, steps, warmup, ev, sample_every=0)
             gbs = nbytes / (ms * 1e-3) / 1e9
             out[name] = {"ms_per_step": round(ms, 4), "GBps": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
                          "stage_ms_with_events": {k: round(v, 4) for k, v in stages.items()}}
@@ -515,7 +541,8 @@ def bench_stream(P, torch, S, ev, dev, distinct=4, reps=3):
     # compute alone, on resident weights
     W13, W2 = torch.from_numpy(w13).to(dev), torch.from_numpy(w2).to(dev)
     desc = H.layer_desc(W13, W2, w.hidden, w.inter, w.types[0], w.types[2])
-    ms_c, _, _ = time_layer(P, torch, [desc], x, tw_d, slot_d, L.MODE_GROUPED, reps * nl, 2, ev, breakdown_steps=1)
+    ms_c, _, _, _ = time_layer(P, torch, [desc], x, tw_d, slot_d, L.MODE_GROUPED, reps * nl, 2, ev, breakdown_steps=1,
+                               sample_every=0)
     del W13, W2
     # the pipeline: nl layers, one group each
     items = [(i, x, tw_d, slot_d) for i in range(nl)]

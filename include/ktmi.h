@@ -148,7 +148,7 @@ int ktmi_moe_layer_noalloc(const ktmi_layer* layer, const void* x, const float* 
  * ktmi_moe_layer calls on this thread record on their stream at the stage boundaries:
  * [0] start, [1] gate/up start (after route sort or x quantisation), [2] gate/up end,
  * [3] down start (after SiLU*mul + q8_1 on the GEMV path), [4] down end, [5] combine end.
- * events = NULL or n = 0 turns it off. */
+ * A NULL entry is not recorded. events = NULL or n = 0 turns it off. */
 #define KTMI_STAGE_EVENTS 6
 int ktmi_set_stage_events(void* const* events, int n);
 
