@@ -108,7 +108,9 @@ def time_layer(P, torch, desc_list, x, w, slot, mode, steps, warmup, ev: HipEven
     nb = breakdown_steps or steps
     se = ev.create(2)
     stage_ev = ev.create(nb * L.STAGE_EVENTS)
-    sampled = [i for i in range(steps) if i % sample_every == sample_every - 1] if sample_every else []
+    sampled = []
+    if sample_every and steps > 0:  # at least the last step when there are fewer than sample_every
+        sampled = [i for i in range(steps) if i % sample_every == sample_every - 1] or [steps - 1]
     kev = ev.create(4 * len(sampled)) if sampled else []  # gate/up start, end, down start, end (boundaries 1-4)
     for i in range(warmup):
         H.moe_layer(desc_list[i % len(desc_list)], x, w, slot, mode, out, ws)
