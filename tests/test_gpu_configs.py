@@ -76,6 +76,15 @@ def test_prefill_chunks(dev, T):
     _check(dev, "q4_k+q6_k-h2048-n512-e256-k8-hot40-prefill", T, L.MODE_GROUPED, max(1, T // 256))
 
 
+@pytest.mark.parametrize("name,T", [("q8_0-h2048-n768-e128-k8-hot16", 4096),
+                                    ("q4_k-h2048-n512-e256-k8-hot32-decode", 8192)])
+def test_256_route_tiles_other_types(dev, name, T):
+    """Chunks long enough for 256-route tiles (per-wave epilogue staging) with the Q8_0 GEMMs
+    and with Q4_K in the down GEMM, which the headline shapes do not reach."""
+    L, _, _ = _pkg()
+    _check(dev, name, T, L.MODE_GROUPED, max(1, T // 96))
+
+
 def test_iq3_s_16k_chunk(dev):
     L, _, _ = _pkg()
     _check(dev, "iq3_s-h2048-n512-e512-k10-hot48", 16384, L.MODE_GROUPED, 64)
