@@ -252,9 +252,10 @@ constexpr int gemm_waves_per_simd() { return FJ == 8 || TYPE == GGML_Q6_K || TYP
 // spread over the sub-steps. Loads past the last step re-read the last one (clamped,
 // unused), keeping the loop branch-free.
 //
-// Epilogue: the accumulators are converted (GATEUP: silu(gate) * up) into a bf16 C tile in
-// LDS over the activation buffers, then written out as whole rows (the down GEMM's rows
-// scatter to Y[perm[m]], whose indices the prologue put in LDS).
+// Epilogue: the accumulators are converted (GATEUP: silu(gate) * up) to bf16 and written
+// out as row segments (the down GEMM's rows scatter to Y[perm[m]], whose indices the
+// prologue put in LDS): at 256-route tiles through a staging area of each wave's own, at
+// 128-route tiles through a C tile in LDS over the activation buffers.
 template <int TYPE, bool GATEUP, int FJ>
 __global__ __launch_bounds__(NTHREADS, (gemm_waves_per_simd<TYPE, FJ>()))
 void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const int32_t* __restrict__ perm,
@@ -489,9 +490,10 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
     }
   };
 
-  // The bf16 C tile is staged in LDS over the activation buffers (rows of CW 16-byte
-  // chunks, chunk c of row r at slot c ^ (r % CW)), then written out as whole rows, 16 bytes
-  // per lane (each row's segment by consecutive lanes: full cache lines per instruction).
+  // 128-route tiles: the bf16 C tile is staged in LDS over the activation buffers (rows of
+  // CW 16-byte chunks, chunk c of row r at slot c ^ (r % CW)), then written out as whole
+  // rows, 16 bytes per lane (each row's segment by consecutive lanes: full cache lines per
+  // instruction).
   // Accumulator layout: lane l holds route 32 j + l % 32 and weight rows
   // 8 (r / 4) + 4 (l / 32) + r % 4 of fragment i: 4 consecutive columns per (i, j, r / 4).
   constexpr int CCOLS = GATEUP ? BNW / 2 : BNW;  // output columns of a tile
