@@ -234,3 +234,31 @@ def test_layer_in_hip_graph(dev, mode):
         assert torch.equal(out, ref), f"replay {r}"
         H.moe_layer(desc, x2, twd, sd, m)  # eager work between the replays
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("mode,T", [("grouped", 48), ("grouped", 4096), ("gemv", 8), ("gemv", 64)])
+def test_slot_address_table_matches_contiguous_slots(dev, mode, T):
+    """Slots given as a device table of per-slot addresses (w_is_table, each slot its own
+    allocation, in reverse order) give the same bits as the contiguous slot tensors: 128- and
+    256-route grouped tiles, the fused decode layer and the stage-by-stage GEMV layer."""
+    import torch
+
+    L, H, S = _pkg()
+    w = S.WORKLOADS["q4_k+q6_k-h2048-n512-e256-k8-hot40-prefill"]
+    _, tw, slot, _ = S.routing(w, T)
+    xb = S.activations(w, T)
+    w13, w2 = S.slot_tensors(w)
+    W13, W2 = to_dev(w13, dev), to_dev(w2, dev)
+    m = L.MODE_GEMV if mode == "gemv" else L.MODE_GROUPED
+    x, twd, sd = bf16_tensor(xb, dev), to_dev(tw, dev), to_dev(slot, dev)
+    ref = H.moe_layer(H.layer_desc(W13, W2, w.hidden, w.inter, w.types[0], w.types[2]), x, twd, sd, m)
+    n = W13.shape[0]
+    p13 = [None] * n
+    p2 = [None] * n
+    for s in reversed(range(n)):
+        p13[s], p2[s] = W13[s].clone(), W2[s].clone()
+    t13 = torch.tensor([p.data_ptr() for p in p13], dtype=torch.int64, device=dev)
+    t2 = torch.tensor([p.data_ptr() for p in p2], dtype=torch.int64, device=dev)
+    got = H.moe_layer(H.layer_desc(t13, t2, w.hidden, w.inter, w.types[0], w.types[2], table=True), x, twd, sd, m)
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16_bits_of(got), bf16_bits_of(ref))
