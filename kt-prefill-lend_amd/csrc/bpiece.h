@@ -58,8 +58,22 @@ __device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
 template <int TYPE>
 struct BPiece;
 
+// lookup<SUB>() issues a piece's codebook reads, convert<SUB>() does the rest of decode<SUB>()
+// with them (a kernel can put the reads ahead of other LDS traffic). Formats without a
+// codebook read nothing there.
+template <class P>
+struct NoLookup {
+  struct Look {};
+  template <int SUB, class Head, class Raw>
+  __device__ static void lookup(const Head&, const Raw&, const uint32_t*, Look&) {}
+  template <int SUB, class Head, class Raw>
+  __device__ static void convert(const Head& hd, const Raw& r, const uint32_t* grid, const Look&, uint32_t out[16]) {
+    P::template decode<SUB>(hd, r, grid, out);
+  }
+};
+
 template <>
-struct BPiece<GGML_Q4_K> {
+struct BPiece<GGML_Q4_K> : NoLookup<BPiece<GGML_Q4_K>> {
   static constexpr int NLOAD = 1;  // VMEM instructions per load<SUB>, at least
   static constexpr int VPM = 4;    // VALU instructions the GEMM schedule places after each MFMA
   struct Head { u32x4_t hdr; };  // d, dmin, scales[12]
@@ -103,7 +117,7 @@ struct BPiece<GGML_Q4_K> {
 };
 
 template <>
-struct BPiece<GGML_Q8_0> {
+struct BPiece<GGML_Q8_0> : NoLookup<BPiece<GGML_Q8_0>> {
   static constexpr int NLOAD = 3;  // VMEM instructions per load<SUB>, at least
   static constexpr int VPM = 4;    // VALU instructions the GEMM schedule places after each MFMA
   struct Head {};
@@ -142,7 +156,7 @@ struct BPiece<GGML_Q8_0> {
 };
 
 template <>
-struct BPiece<GGML_Q6_K> {
+struct BPiece<GGML_Q6_K> : NoLookup<BPiece<GGML_Q6_K>> {
   static constexpr int NLOAD = 4;  // VMEM instructions per load<SUB>, at least
   static constexpr int VPM = 5;    // VALU instructions the GEMM schedule places after each MFMA
   // the 20 bytes from the dword below scales[0]: scales[16] and d, s = byte shift
@@ -246,38 +260,59 @@ struct BPiece<GGML_IQ3_S> {
     r.sg[1] = s2[1];
     r.qh = gload<uint32_t>(dword_floor(b + 66 + ib));
   }
+  // the 8 codebook entries of the piece's 4-value groups
+  struct Look { uint32_t g[8]; };
   template <int SUB>
-  __device__ static void decode(const Head& hd, const Raw& r, const uint32_t* grid, uint32_t out[16]) {
+  __device__ static void lookup(const Head& hd, const Raw& r, const uint32_t* grid, Look& lk) {
     const uint32_t s = hd.s;
     const uint32_t h = (threadIdx.x >> 5) & 1;
     const int ib = 2 * SUB + (int)h;
-    // block byte offsets: qs at 2 + 8 ib, signs at 74 + 4 ib (both = s + 2 mod 4),
-    // qh at 66 + ib, scales at 106, d at 0
+    // block byte offsets: qs at 2 + 8 ib (= s + 2 mod 4), qh at 66 + ib
     const uint32_t s2 = (s + 2) & 3;
     const uint32_t qs0 = alignbyte(r.qs[1], r.qs[0], s2), qs1 = alignbyte(r.qs[2], r.qs[1], s2);
-    const uint32_t sg = alignbyte(r.sg[1], r.sg[0], s2);
     const uint32_t qh = (r.qh >> (8 * ((s + 2 + ib) & 3))) & 0xFF;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t qsb = ((k < 4 ? qs0 : qs1) >> (8 * (k & 3))) & 0xFF;
+      lk.g[k] = grid[qsb | (((qh >> k) & 1) << 8)];
+    }
+  }
+  template <int SUB>
+  __device__ static void convert(const Head& hd, const Raw& r, const uint32_t*, const Look& lk, uint32_t out[16]) {
+    const uint32_t s = hd.s;
+    const uint32_t h = (threadIdx.x >> 5) & 1;
+    const int ib = 2 * SUB + (int)h;
+    // block byte offsets: signs at 74 + 4 ib (= s + 2 mod 4), scales at 106, d at 0
+    const uint32_t s2 = (s + 2) & 3;
+    const uint32_t sg = alignbyte(r.sg[1], r.sg[0], s2);
     const uint32_t scw = alignbyte(hd.sc1, hd.sc0, s2);  // scales[0..3]
     const uint32_t nib = (scw >> (8 * (ib >> 1) + 4 * (ib & 1))) & 15;
     const uint32_t dbits = (hd.dw >> (8 * s)) & 0xFFFF;
     const float db = half_bits_to_float(dbits) * (float)(1 + 2 * (int)nib);
-    // value j of group k takes sign bit 4k + j of sg: (sign ? -v : v) with v = db * grid byte
-    // (whose sign bit is db's, zero included) has the sign bit sg[4k + j] XOR sign(db), so the
-    // sign goes in with one shift and one bitfield insert
-    const uint32_t sgx = sg ^ (uint32_t)((int32_t)__float_as_uint(db) >> 31);
+    // value 4k + j takes sign bit 4k + j of sg. (sign ? -v : v) of v = db * grid byte flips
+    // the sign bit of v, and so of its bf16 rounding: the pair of values 2p, 2p + 1 is
+    // packed first, then bits 2p and 2p + 1 of sg are moved to bits 15 and 31 by one packed
+    // 16-bit shift of sg's half-word (in both halves) and xored in
+    const uint32_t sgw[2] = {(sg & 0xFFFFu) | (sg << 16), (sg >> 16) | (sg & 0xFFFF0000u)};
+    auto pair_signs = [&](int p) {
+      const int q = (2 * p) & 15;
+      const u16x2_t v = __builtin_bit_cast(u16x2_t, sgw[p >> 3]) << u16x2_t{(uint16_t)(15 - q), (uint16_t)(14 - q)};
+      return __builtin_bit_cast(uint32_t, v) & 0x80008000u;
+    };
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const uint32_t qsb = ((k < 4 ? qs0 : qs1) >> (8 * (k & 3))) & 0xFF;
-      const uint32_t g = grid[qsb | (((qh >> k) & 1) << 8)];
       float y[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float v = db * (float)((g >> (8 * j)) & 0xFF);
-        y[j] = __uint_as_float(bfi(0x80000000u, sgx << (31 - (4 * k + j)), __float_as_uint(v)));
-      }
-      out[2 * k] = f2bf2(y[0], y[1]);
-      out[2 * k + 1] = f2bf2(y[2], y[3]);
+      for (int j = 0; j < 4; ++j) y[j] = db * (float)((lk.g[k] >> (8 * j)) & 0xFF);
+      out[2 * k] = f2bf2(y[0], y[1]) ^ pair_signs(2 * k);
+      out[2 * k + 1] = f2bf2(y[2], y[3]) ^ pair_signs(2 * k + 1);
     }
+  }
+  template <int SUB>
+  __device__ static void decode(const Head& hd, const Raw& r, const uint32_t* grid, uint32_t out[16]) {
+    Look lk;
+    lookup<SUB>(hd, r, grid, lk);
+    convert<SUB>(hd, r, grid, lk, out);
   }
   __device__ static int off0(int h) { return 32 * h; }
   __device__ static int off1(int h) { return 32 * h + 16; }

@@ -27,6 +27,7 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
 // the same vectors with 4-byte alignment (36-byte q8_1 blocks, 2-byte aligned GGUF blocks
 // read from the dword below them)
 typedef uint32_t u32x4_a4_t __attribute__((ext_vector_type(4))) __attribute__((aligned(4)));

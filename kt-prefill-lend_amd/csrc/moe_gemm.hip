@@ -433,6 +433,11 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
     for (int j = 0; j < FJ; ++j) af[0][j] = *(const bf16x8_t*)(Ab + j * 32 * A_ROW + a_rd[0]);
 #pragma unroll
     for (int s2 = 0; s2 < 4; s2 += 2) {
+      // the codebook reads (IQ3_S) of the piece this region decodes, ahead of the region's
+      // activation reads: the decode then waits only for them, not for every LDS read
+      const typename BP::Head& hd1 = SUB == 3 ? head_nxt[s2 / 2] : head[s2 / 2];
+      typename BP::Look look;
+      BP::template lookup<SUB1>(hd1, raw[cur ^ 1][s2 / 2], grid_lds, look);
       __builtin_amdgcn_sched_barrier(0);
       issue_a(sb3, std::integral_constant<int, SUB3>{}, anext, (s2 / 2) * AJ / 2, (s2 / 2 + 1) * AJ / 2);
       BP::template load<SUB2>(b_row[s2 / 2], sb2, h, grid_lds, raw[cur][s2 / 2]);
@@ -458,8 +463,7 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
           for (int j = 0; j < FJ; ++j) af[0][j] = *(const bf16x8_t*)(Ab + j * 32 * A_ROW + a_rd[2]);
         }
       }
-      BP::template decode<SUB1>(SUB == 3 ? head_nxt[s2 / 2] : head[s2 / 2], raw[cur ^ 1][s2 / 2], grid_lds,
-                                wv[cur ^ 1][s2 / 2]);
+      BP::template convert<SUB1>(hd1, raw[cur ^ 1][s2 / 2], grid_lds, look, wv[cur ^ 1][s2 / 2]);
       // schedule: the direct loads first, then 32 x (1 MFMA, VPM VALU), an LDS read after
       // every other MFMA and one of the raw weight gathers after every other (each
       // gathers 32 rows' cache lines: in one burst they would hold up the MFMA issue).
