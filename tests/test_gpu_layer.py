@@ -112,6 +112,20 @@ def test_fused_decode_every_type(dev, case):
     assert np.all(got[(slot < 0).all(axis=1)] == 0)
 
 
+@pytest.mark.parametrize("T", [32, 33])
+def test_decode_at_the_fused_route_limit(dev, T):
+    """GEMV mode at 256 routes (32 tokens x 8: the most the fused decode launches take) and at
+    264 (33 tokens: the stage-by-stage GEMV sequence), against the oracle's restatement of
+    the reference kernels' sequence."""
+    L, _, _ = _pkg()
+    w, xb, tw, slot, w13, w2 = _case("q4_k-h2048-n512-e256-k8-hot32-decode", T, 512, 256, 8, 32)
+    got = R.bf16_to_f32(_run(dev, w, xb, tw, slot, w13, w2, L.MODE_GEMV))
+    exp = R.bf16_to_f32(gemv_layer_oracle(xb, tw, slot, w13, w2, w.types, w.hidden, w.inter))
+    l2, _, _ = R.rel_errors(got, exp)
+    assert l2 < 4e-3, l2
+    assert np.all(got[(slot < 0).all(axis=1)] == 0)
+
+
 @pytest.mark.parametrize("mode", ["gemv", "grouped"])
 def test_layer_deterministic(dev, mode):
     L, _, _ = _pkg()
@@ -138,6 +152,24 @@ def test_grouped_edge_cases(dev):
         if T > 1:
             l2, _, _ = R.rel_errors(got, ref)
             assert l2 < TOL_REL_L2
+
+
+def test_grouped_past_the_combine_grid_limit(dev):
+    """70000 tokens (560k routes, hidden 256): the combine runs in slices of 65535 tokens (the
+    grid's y limit). Tokens past the first slice equal a call on those tokens alone, bit for
+    bit (a token's output depends only on its own routes), and a token sample from both
+    slices matches the fp64 FFN."""
+    L, _, _ = _pkg()
+    T, cut = 70000, 65535
+    w, xb, tw, slot, w13, w2 = _case("q4_k+q6_k-h2048-n512-e256-k8-hot40-prefill", T, 256, 256, 8, 32)
+    y = _run(dev, w, xb, tw, slot, w13, w2, L.MODE_GROUPED)
+    tail = _run(dev, w, xb[cut:], tw[cut:], slot[cut:], w13, w2, L.MODE_GROUPED)
+    assert np.array_equal(y[cut:], tail)
+    g, d = dequant_w(w13, w2, w.types, w.hidden, w.inter)
+    sample = np.concatenate([np.arange(0, cut, 2049), np.arange(cut - 3, T, 157)])
+    ref = R.ffn_reference(xb[sample], slot[sample], tw[sample], g, d)
+    l2, l1, cos = R.rel_errors(R.bf16_to_f32(y[sample]), ref)
+    assert l2 < TOL_REL_L2 and cos > 0.999, (l2, l1, cos)
 
 
 def test_grouped_at_full_shape(dev):
