@@ -467,8 +467,9 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
       // schedule: the direct loads first, then 32 x (1 MFMA, VPM VALU), an LDS read after
       // every other MFMA and one of the raw weight gathers after every other (each
       // gathers 32 rows' cache lines: in one burst they would hold up the MFMA issue).
-      // VPM covers the type's decode (Q4_K and Q8_0 about 3.5 VALU per MFMA, Q6_K 4.3,
-      // IQ3_S 7): VALU left over would run after the last MFMA with the matrix core idle.
+      // VPM covers the type's decode (Q4_K and Q8_0 about 3.5 VALU per MFMA, Q6_K 4.1,
+      // IQ3_S 4.3 once its codebook reads are out of the region): VALU left over would run
+      // after the last MFMA with the matrix core idle.
       __builtin_amdgcn_sched_group_barrier(0x020, AJ / 2, 0);
 #pragma unroll
       for (int m = 0; m < NMR; ++m) {
