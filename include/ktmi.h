@@ -131,6 +131,14 @@ int ktmi_moe_layer(const ktmi_layer* layer, const void* x, const float* topk_w, 
                    void* stream);
 /* The mode KTMI_MODE_AUTO picks for this many routes. */
 int ktmi_moe_layer_mode(const ktmi_layer* layer, int64_t tokens, int64_t top_k);
+/* Tokens per pass of KTMI_MODE_GROUPED: a longer call runs as consecutive passes over token
+ * slices of this size (each token's output depends only on its own routes), and the
+ * workspace covers one pass. The grouped kernels address x [T, hidden], H [T top_k, inter]
+ * and Y [T top_k, hidden] (bf16) with 32-bit offsets, so a pass is the largest multiple of
+ * 256 tokens with 2 top_k max(hidden, inter) T < 4 GiB - 64 KiB: 37376 tokens at hidden 7168
+ * and top-8, 130816 at hidden 2048 and top-8. No counterpart in the reference, whose torch
+ * path has no such limit. */
+int64_t ktmi_moe_layer_pass_tokens(const ktmi_layer* layer, int64_t top_k);
 
 /* ktmi_moe_layer without a workspace argument. No counterpart in the reference: this is for
  * callers that cannot allocate device memory (code under HIP graph capture, tight serving
@@ -215,7 +223,7 @@ int ktmi_host_free(void* p);
  * (ktmi_bank, host memory that outlives the engine); expert ids index the bank, other ids
  * (-1 for the GPU's residents) add nothing. Types: 8, 12, 14, 21. */
 typedef struct ktmi_cpu_moe ktmi_cpu_moe;
-/* threads <= 0: min(16, host threads) - 1. max_tokens x max_top_k sizes the pinned staging
+/* threads <= 0: the CPUs of the process affinity mask, minus one. max_tokens x max_top_k sizes the pinned staging
  * of submit (0 for a forward-only engine). Replaces kt-kernel's MOE construction and
  * KExpertsCPUBuffer (the wrapper's CPU side). NULL on failure. */
 ktmi_cpu_moe* ktmi_cpu_moe_create(int64_t hidden, int64_t inter, int type13, int type2, const ktmi_bank* bank,
@@ -235,6 +243,12 @@ int ktmi_cpu_moe_submit(ktmi_cpu_moe* h, const void* x_bf16, const int32_t* expe
  * kt_uva_handoff.sync_add (P:10598-10602, P:41285-41301). */
 int ktmi_cpu_moe_sync_add(ktmi_cpu_moe* h, void* out_bf16, void* stream);
 int ktmi_cpu_moe_threads(const ktmi_cpu_moe* h);
+/* The bound (microseconds, default 10 s) on how long the add that sync_add enqueues ahead of
+ * a decode window's CPU side waits for it. An add that waits longer writes NaN into the
+ * layer's rows, exits, and sync_add returns KTMI_EHIP. No counterpart in the reference,
+ * whose add waits without a bound (sync_with_cuda_stream, P:41294). Not while a submit is
+ * outstanding. */
+int ktmi_cpu_moe_set_add_wait(ktmi_cpu_moe* h, int64_t microseconds);
 /* "avx512-vnni" or "scalar": the engine's int8 dot-product kernels (VNNI when the host has
  * it, unless KTMI_CPU_ISA=scalar was set at creation) */
 const char* ktmi_cpu_moe_isa(const ktmi_cpu_moe* h);

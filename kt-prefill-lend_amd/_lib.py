@@ -64,6 +64,7 @@ SIGNATURES = {
     "ktmi_moe_layer_workspace": (_i64, [C.POINTER(ktmi_layer), _i64, _i64, _i32]),
     "ktmi_moe_layer": (_i32, [C.POINTER(ktmi_layer), _vp, _vp, _vp, _i64, _i64, _vp, _vp, _i64, _i32, _vp]),
     "ktmi_moe_layer_mode": (_i32, [C.POINTER(ktmi_layer), _i64, _i64]),
+    "ktmi_moe_layer_pass_tokens": (_i64, [C.POINTER(ktmi_layer), _i64]),
     "ktmi_moe_layer_noalloc": (_i32, [C.POINTER(ktmi_layer), _vp, _vp, _vp, _i64, _i64, _vp, _i32, _vp]),
     "ktmi_set_stage_events": (_i32, [C.POINTER(C.c_void_p), _i32]),
     "ktmi_quantize_rows_host": (_i32, [_vp, _i64, _i64, _i32, _vp, _i32]),
@@ -86,6 +87,7 @@ SIGNATURES = {
     "ktmi_cpu_moe_sync_add": (_i32, [_vp, _vp, _vp]),
     "ktmi_cpu_moe_threads": (_i32, [_vp]),
     "ktmi_cpu_moe_isa": (C.c_char_p, [_vp]),
+    "ktmi_cpu_moe_set_add_wait": (_i32, [_vp, _i64]),
 }
 
 _lib = None

@@ -208,13 +208,31 @@ static int check_layer(const ktmi_layer* L) {
   return KTMI_OK;
 }
 
+// Tokens per pass of the grouped mode. Its kernels address x [T, K], H [R, N] and Y [R, K]
+// (bf16, R = T top_k) with 32-bit buffer offsets, and an offset at 0xFFFFFFF0 marks a store
+// to drop; a pass keeps every one of them under 4 GiB - 64 KiB. A token's output depends only
+// on its own routes, so a longer layer runs as consecutive passes over token slices, each
+// with the whole workspace.
+static int64_t grouped_pass_tokens(const ktmi_layer* L, int64_t top_k) {
+  const int64_t limit = 0xFFFF0000ll;
+  const int64_t per_token = 2 * top_k * (L->hidden > L->inter ? L->hidden : L->inter);
+  const int64_t t = limit / per_token;
+  return t >= 256 ? t / 256 * 256 : (t > 0 ? t : 1);
+}
+
+int64_t ktmi_moe_layer_pass_tokens(const ktmi_layer* L, int64_t top_k) {
+  if (!L || top_k <= 0 || L->hidden <= 0 || L->inter <= 0) return 0;
+  return grouped_pass_tokens(L, top_k);
+}
+
 int64_t ktmi_moe_layer_workspace(const ktmi_layer* L, int64_t tokens, int64_t top_k, int mode) {
   if (!L || tokens < 0 || top_k <= 0) return 0;
   if (mode == KTMI_MODE_AUTO) mode = ktmi_moe_layer_mode(L, tokens, top_k);
   if (mode == KTMI_MODE_GEMV)
     return decode_layer_fits(L, tokens, top_k) ? decode_layer_workspace(L, tokens, top_k)
                                                : gemv_layer_workspace(L, tokens, top_k);
-  return grouped_plan(tokens, top_k, L->n_slots, L->hidden, L->inter).total;
+  const int64_t pass = grouped_pass_tokens(L, top_k);
+  return grouped_plan(tokens < pass ? tokens : pass, top_k, L->n_slots, L->hidden, L->inter).total;
 }
 
 int ktmi_moe_layer(const ktmi_layer* L, const void* x, const float* topk_w, const int32_t* slot_ids, int64_t tokens,
@@ -270,9 +288,15 @@ int ktmi_moe_layer(const ktmi_layer* L, const void* x, const float* topk_w, cons
     return rc;
   }
   KTMI_REQUIRE(mode == KTMI_MODE_GROUPED, KTMI_EINVAL, "moe_layer: mode %d", mode);
-  GroupedPlan P = grouped_plan(tokens, top_k, L->n_slots, K, N);
-  return launch_grouped_layer(L, (const uint16_t*)x, topk_w, slot_ids, tokens, top_k, (uint16_t*)y,
-                              (uint8_t*)workspace, P, s);
+  const int64_t pass = grouped_pass_tokens(L, top_k);
+  for (int64_t t0 = 0; t0 < tokens; t0 += pass) {
+    const int64_t nt = tokens - t0 < pass ? tokens - t0 : pass;
+    const GroupedPlan P = grouped_plan(nt, top_k, L->n_slots, K, N);
+    rc = launch_grouped_layer(L, (const uint16_t*)x + t0 * K, topk_w + t0 * top_k, slot_ids + t0 * top_k, nt, top_k,
+                              (uint16_t*)y + t0 * K, (uint8_t*)workspace, P, s);
+    if (rc) return rc;
+  }
+  return KTMI_OK;
 }
 
 int ktmi_moe_layer_noalloc(const ktmi_layer* L, const void* x, const float* topk_w, const int32_t* slot_ids,

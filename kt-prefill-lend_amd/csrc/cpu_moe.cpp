@@ -32,6 +32,7 @@
 #include <vector>
 
 #include <immintrin.h>
+#include <sched.h>
 
 namespace ktmi_cpu {
 namespace {
@@ -561,6 +562,18 @@ int64_t row_block(int64_t rows, int64_t experts, int threads) {
   return rows % best ? rows : best;
 }
 
+// CPUs in this process's affinity mask (what a container or job scheduler grants), or the
+// hardware's count where the mask cannot be read
+int usable_cpus() {
+  cpu_set_t set;
+  CPU_ZERO(&set);
+  if (sched_getaffinity(0, sizeof set, &set) == 0) {
+    const int n = CPU_COUNT(&set);
+    if (n > 0) return n;
+  }
+  return (int)std::max(1u, std::thread::hardware_concurrency());
+}
+
 }  // namespace
 
 struct Engine {
@@ -592,9 +605,9 @@ Engine* engine_create(int64_t hidden, int64_t inter, int64_t n_experts, int type
   if (hidden % block_of(type13) || inter % block_of(type2) || hidden % 256 || inter % 32)
     return fail("hidden / intermediate are not whole blocks of the weight and activation types");
   if (!gate || !up || !down) return fail("null bank pointer");
-  // default: 16 host threads at most, one of them left to the thread that drives the GPU
-  if (threads <= 0)
-    threads = (int)std::max<unsigned>(1u, std::min<unsigned>(16, std::max(1u, std::thread::hardware_concurrency())) - 1);
+  // default: the CPUs this process may run on (its affinity mask), one of them left to the
+  // thread that drives the GPU
+  if (threads <= 0) threads = std::max(1, usable_cpus() - 1);
   Engine* e = new Engine(threads);
   e->K = hidden;
   e->N = inter;

@@ -29,9 +29,15 @@
 
 // sync_add enqueues its add ahead of the CPU side's end for layers of at most this many
 // tokens (decode windows, whose CPU side takes milliseconds); that add waits at most
-// KTMI_WAIT_ADD_SECONDS for the CPU side. Larger layers are added once the CPU side is done.
+// KTMI_WAIT_ADD_US (ktmi_cpu_moe_set_add_wait changes it) for the CPU side. Larger layers
+// are added once the CPU side is done.
 constexpr int64_t KTMI_WAIT_ADD_MAX_TOKENS = 256;
-constexpr uint64_t KTMI_WAIT_ADD_SECONDS = 10;
+constexpr int64_t KTMI_WAIT_ADD_US = 10 * 1000 * 1000;
+
+static int64_t host_ns() {
+  return std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now().time_since_epoch())
+      .count();
+}
 
 struct ktmi_cpu_moe {
   ktmi_cpu::Engine* eng = nullptr;
@@ -58,6 +64,10 @@ struct ktmi_cpu_moe {
   uint32_t* fin_h = nullptr;
   uint32_t* fin_hd = nullptr;
   uint64_t wait_ticks = 0;  // that add's wait bound, in wall-clock ticks
+  int64_t wait_us = 0;      // the same bound in microseconds
+  int wall_khz = 0;         // the GPU wall clock's rate
+  // host clock when the worker published the last completion word (after fin[0])
+  std::atomic<int64_t> done_ns{0};
   hipEvent_t in_ready = nullptr;
   // out_free[s & 1]: submit s's add is done with the pinned output. Two, so that sync_add of
   // submit s, which may enqueue its add before the worker has started on s, never re-records
@@ -203,6 +213,7 @@ void worker_loop(ktmi_cpu_moe* h) {
     // the output's stores before the completion words (an add kernel may be waiting on them)
     if (rc == 0) __atomic_store_n(h->fin_h + 1, h->seq, __ATOMIC_RELEASE);
     __atomic_store_n(h->fin_h, h->seq, __ATOMIC_RELEASE);
+    h->done_ns.store(host_ns());
     {
       std::lock_guard<std::mutex> g(h->m);
       h->state.store(ktmi_cpu_moe::DONE);
@@ -296,7 +307,9 @@ ktmi_cpu_moe* ktmi_cpu_moe_create(int64_t hidden, int64_t inter, int type13, int
     if (e == hipSuccess) e = hipHostGetDevicePointer((void**)&h->fin_hd, h->fin_h, 0);
     int khz = 0;
     if (e == hipSuccess) e = hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, h->device);
-    h->wait_ticks = (uint64_t)(khz > 0 ? khz : 100000) * 1000ull * KTMI_WAIT_ADD_SECONDS;
+    h->wall_khz = khz > 0 ? khz : 100000;
+    h->wait_us = KTMI_WAIT_ADD_US;
+    h->wait_ticks = (uint64_t)h->wall_khz * (uint64_t)h->wait_us / 1000ull;
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e == hipSuccess) {
       __atomic_store_n(h->seq_h, 0u, __ATOMIC_RELEASE);
@@ -319,6 +332,18 @@ int ktmi_cpu_moe_destroy(ktmi_cpu_moe* h) {
 }
 
 int ktmi_cpu_moe_threads(const ktmi_cpu_moe* h) { return h ? ktmi_cpu::engine_threads(h->eng) : 0; }
+
+int ktmi_cpu_moe_set_add_wait(ktmi_cpu_moe* h, int64_t microseconds) {
+  clear_error();
+  KTMI_REQUIRE(h && h->fin_h, KTMI_EINVAL, "cpu_moe_set_add_wait: no engine with a handoff");
+  KTMI_REQUIRE(microseconds >= 1 && microseconds <= 3600ll * 1000 * 1000, KTMI_EINVAL,
+               "cpu_moe_set_add_wait: %lld us (1 us .. 1 h)", (long long)microseconds);
+  std::lock_guard<std::mutex> g(h->m);
+  KTMI_REQUIRE(h->state == ktmi_cpu_moe::IDLE, KTMI_EINVAL, "cpu_moe_set_add_wait: a submitted layer is not synced");
+  h->wait_us = microseconds;
+  h->wait_ticks = (uint64_t)h->wall_khz * (uint64_t)microseconds / 1000ull;
+  return KTMI_OK;
+}
 
 const char* ktmi_cpu_moe_isa(const ktmi_cpu_moe* h) { return h ? ktmi_cpu::engine_isa(h->eng) : ""; }
 
@@ -386,6 +411,7 @@ int ktmi_cpu_moe_sync_add(ktmi_cpu_moe* h, void* out_bf16, void* stream) {
   // completion word.
   const bool ahead = T > 0 && T <= KTMI_WAIT_ADD_MAX_TOKENS && out_ok;
   hipError_t early = hipSuccess;
+  const int64_t enq_ns = host_ns();  // the add's blocks start after this
   if (ahead) {
     const int64_t n = T * h->K;
     wait_add_kernel<<<(unsigned)(((n + 7) / 8 + 255) / 256), 256, 0, (hipStream_t)stream>>>(
@@ -406,9 +432,19 @@ int ktmi_cpu_moe_sync_add(ktmi_cpu_moe* h, void* out_bf16, void* stream) {
   if (T == 0) return KTMI_OK;
   KTMI_REQUIRE(out_ok, KTMI_EINVAL, "cpu_moe_sync_add: output null or not 16-byte aligned");
   if (ahead) {
-    KTMI_REQUIRE(__atomic_load_n(h->fin_h + 2, __ATOMIC_ACQUIRE) != seq, KTMI_EHIP,
-                 "cpu_moe_sync_add: the add stopped waiting for the CPU side after %llu s",
-                 (unsigned long long)KTMI_WAIT_ADD_SECONDS);
+    // Did any block of the add give up? Each block starts its bound after enq_ns and sees
+    // the completion word within microseconds of the worker's store (done_ns): a worker
+    // done less than half a bound of at least 1 ms after enq_ns leaves every block time to
+    // spare, and no block gave up. Otherwise the blocks' outcome is read once the add has
+    // finished: a block that gives up records it in fin[2] before it exits, so a block
+    // still deciding cannot be missed.
+    const int64_t done_after_us = (h->done_ns.load() - enq_ns) / 1000;
+    if (!(h->wait_us >= 1000 && done_after_us < h->wait_us / 2)) {
+      KTMI_HIP_TRY(hipEventSynchronize(h->out_free[seq & 1]));
+      KTMI_REQUIRE(__atomic_load_n(h->fin_h + 2, __ATOMIC_ACQUIRE) != seq, KTMI_EHIP,
+                   "cpu_moe_sync_add: the add stopped waiting for the CPU side after %lld us (its rows are NaN)",
+                   (long long)h->wait_us);
+    }
     return KTMI_OK;
   }
   const int rc = ktmi_add_bf16(out_bf16, h->out_hd, T * h->K, stream);

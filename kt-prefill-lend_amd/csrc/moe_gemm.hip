@@ -781,9 +781,10 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
                (long long)K, BNW > 256 ? BNW : 256);
   KTMI_REQUIRE(N % (BNW / 2) == 0 && N % 256 == 0, KTMI_EINVAL,
                "grouped layer: intermediate %lld not a multiple of 256", (long long)N);
-  // x, H and Y are addressed by buffer instructions with 32-bit offsets
-  KTMI_REQUIRE(tokens * K * 2 <= 0xFFFFFFFFll && R * N * 2 <= 0xFFFFFFFFll && R * K * 2 <= 0xFFFFFFFFll, KTMI_EINVAL,
-               "grouped layer: activations of %lld tokens exceed the 4 GiB buffer range", (long long)tokens);
+  // x, H and Y are addressed by buffer instructions with 32-bit offsets, 0xFFFFFFF0 marking a
+  // dropped store (the caller splits longer layers into passes that fit)
+  KTMI_REQUIRE(tokens * K * 2 <= 0xFFFF0000ll && R * N * 2 <= 0xFFFF0000ll && R * K * 2 <= 0xFFFF0000ll, KTMI_EINVAL,
+               "grouped layer: a pass of %lld tokens exceeds the 32-bit buffer range", (long long)tokens);
   if (tokens == 0) return KTMI_OK;
   int32_t* hist = (int32_t*)(ws + P.off_counts);
   int32_t* seg = (int32_t*)(ws + P.off_seg);

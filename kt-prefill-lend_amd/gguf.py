@@ -67,7 +67,9 @@ _GV_SCALAR = {GV_UINT8: "<u1", GV_INT8: "<i1", GV_UINT16: "<u2", GV_INT16: "<i2"
 
 
 class GGUFFile:
-    """A GGUF file's metadata and tensor table over a read-only memory map.
+    """A GGUF file's metadata and tensor table over a private (copy-on-write) memory map:
+    arrays over it are writable views, so torch takes them without a read-only warning, and
+    no write through them can reach the file (a written page becomes this process's copy).
 
     metadata: key -> value (numbers, str, or lists for arrays); metadata_types: key -> value
     type; tensors: name -> {"shape": outermost-first dims, "type": ggml type, "offset":
@@ -79,7 +81,7 @@ class GGUFFile:
 
         self.path = path
         with open(path, "rb") as f:
-            self._mm = mmap.mmap(f.fileno(), 0, access=mmap.ACCESS_READ)
+            self._mm = mmap.mmap(f.fileno(), 0, access=mmap.ACCESS_COPY)
         mm = self._mm
         size = len(mm)
 
@@ -185,7 +187,7 @@ class GGUFFile:
         return self.tensors[name]["type"]
 
     def raw(self, name: str) -> np.ndarray:
-        """The tensor's bytes: a read-only uint8 view over the file mapping (no copy)."""
+        """The tensor's bytes: a uint8 view over the private file mapping (no copy)."""
         info = self.tensors[name]
         if info["n_bytes"] is None:
             raise ValueError(f"{self.path}: tensor {name} has ggml type {info['type']} of unknown size")

@@ -57,6 +57,11 @@ class KTCPUExperts:
     def isa(self) -> str:
         return _lib.lib().ktmi_cpu_moe_isa(self._h).decode()
 
+    def set_add_wait(self, microseconds: int) -> None:
+        """Bound on how long the add that sync_add enqueues ahead of a decode window's CPU side
+        waits for it (default 10 s); past it the layer's rows become NaN and sync_add raises."""
+        _lib.check(_lib.lib().ktmi_cpu_moe_set_add_wait(self._h, int(microseconds)), "cpu_moe_set_add_wait")
+
     def close(self):
         if getattr(self, "_h", None):
             _lib.lib().ktmi_cpu_moe_destroy(self._h)

@@ -62,13 +62,8 @@ class GGUFExperts:
         self.num_layers = cfg["num_layers"]
 
     def _raw(self, name: str):
-        """(uint8 torch view of the tensor's bytes over the mapping, ggml type)."""
-        import warnings
-
-        data = self.file.raw(name)
-        with warnings.catch_warnings():
-            warnings.simplefilter("ignore")  # read-only buffer, only copied out
-            return torch.from_numpy(data), self.file.ggml_type(name)
+        """(uint8 torch view of the tensor's bytes over the file's private mapping, ggml type)."""
+        return torch.from_numpy(self.file.raw(name)), self.file.ggml_type(name)
 
     def types(self, layer_idx: int):
         return tuple(self.file.ggml_type(f"blk.{layer_idx}.ffn_{p}_exps.weight") for p in ("gate", "up", "down"))

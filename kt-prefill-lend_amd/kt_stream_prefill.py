@@ -41,7 +41,6 @@ from __future__ import annotations
 import ctypes as C
 import os
 import time
-import traceback
 from dataclasses import dataclass
 from typing import Dict, List, Optional, Sequence, Tuple
 
@@ -394,34 +393,43 @@ class KTStreamPrefillGGUF:
         return outs
 
     def _reference_check(self, layer_idx, x, ids, w, acc, first):
-        """KT_GPU_STREAM_SELFTEST=2 (P:40821-40853): the streamed experts' partial output
-        from a torch fp32 FFN over the bank's experts (dequantised by kt_gguf_dequant), logged
-        against acc. A diagnostic: it does not change the result."""
+        """KT_GPU_STREAM_SELFTEST=2 (the reference's self-check, P:40821-40853): recomputes the
+        streamed experts' share of this layer in fp32 from their bf16-dequantised bank bytes,
+        one routed expert at a time, and logs how far `acc` is from it (relative L2, cosine,
+        largest difference). A diagnostic: `acc` is returned unchanged either way."""
         from . import kt_gguf_dequant as DQ
 
         torch.cuda.current_stream(self.device).synchronize()
-        b, (t13, _, t2) = self.bank(layer_idx), self.types(layer_idx)
+        bank, types = self.bank(layer_idx), self.types(layer_idx)
         N, K = self.N, self.K
-        ref = torch.zeros(acc.shape, dtype=torch.float32, device=self.device)
-        ids64, xf, used = ids.to(torch.int64), x.float(), 0
-        wg = torch.empty((1, N, K), dtype=torch.bfloat16, device=self.device)
-        wu, wd = torch.empty_like(wg), torch.empty((1, K, N), dtype=torch.bfloat16, device=self.device)
-        for e in range(first, b.n_experts):
-            tok, kk = torch.where(ids64 == e)
-            if tok.numel() == 0:
-                continue
-            used += 1
-            for part, dst, t, (r, c) in ((b.gate, wg, t13, (N, K)), (b.up, wu, t13, (N, K)), (b.down, wd, t2, (K, N))):
-                raw = part[e:e + 1].to(self.device)
-                DQ.dequant_experts(raw, raw.shape[1], t, 1, r, c, dst)
-            h = xf[tok]
-            a = torch.nn.functional.silu(h @ wg[0].float().t()) * (h @ wu[0].float().t())
-            ref.index_add_(0, tok, (a @ wd[0].float().t()) * w[tok, kk].float().unsqueeze(1))
-        d = acc.float() - ref
-        cos = torch.nn.functional.cosine_similarity(acc.float().flatten(), ref.flatten(), dim=0).item()
-        rel = (d.norm() / ref.norm().clamp_min(1e-30)).item()
-        _log(f"rank {self.rank}: self-check layer {layer_idx}, {x.shape[0]} tokens, {used} experts: rel L2 {rel:.2e}, "
-             f"cos {cos:.6f}, max |diff| {d.abs().max().item():.4g}")
+        routed = ids.to(device=self.device, dtype=torch.int64)
+        coef_all = w.to(device=self.device, dtype=torch.float32)
+        experts = [e for e in torch.unique(routed).tolist() if first <= e < bank.n_experts]
+        proj = (("gate", bank.gate, types[0], (N, K)), ("up", bank.up, types[1], (N, K)),
+                ("down", bank.down, types[2], (K, N)))
+        expected = torch.zeros(acc.shape, dtype=torch.float32, device=self.device)
+        xf = x.to(torch.float32)
+        for e in experts:
+            wt = {}
+            for name, part, t, (rows, cols) in proj:
+                dq = torch.empty((1, rows, cols), dtype=torch.bfloat16, device=self.device)
+                src = part[e].view(1, -1).to(self.device)
+                DQ.dequant_experts(src, src.shape[1], t, 1, rows, cols, dq)
+                wt[name] = dq[0].to(torch.float32)
+            hit = routed == e  # a token routes to an expert at most once
+            rows_e = hit.any(dim=1).nonzero().squeeze(1)
+            scale = (coef_all * hit).sum(dim=1)[rows_e]
+            xe = xf[rows_e]
+            g = torch.matmul(xe, wt["gate"].t())
+            act = g * torch.sigmoid(g) * torch.matmul(xe, wt["up"].t())
+            expected[rows_e] += torch.matmul(act, wt["down"].t()) * scale[:, None]
+        got = acc.to(torch.float32)
+        rel = ((got - expected).norm() / expected.norm().clamp_min(1e-30)).item()
+        cos = (torch.dot(got.flatten(), expected.flatten())
+               / (got.norm() * expected.norm()).clamp_min(1e-30)).item()
+        worst = (got - expected).abs().max().item() if got.numel() else 0.0
+        _log(f"rank {self.rank}: self-check of layer {layer_idx} over {x.shape[0]} tokens and {len(experts)} "
+             f"streamed experts: rel L2 {rel:.2e}, cos {cos:.6f}, max |diff| {worst:.4g}")
         return rel, cos
 
     def copy_stream(self) -> int:
@@ -467,36 +475,55 @@ def preallocate(layer) -> None:
     _log(f"preallocated 2 slots of {GROUP_SIZE} experts and the workspace for {T} rows ({mb:.0f} MB) on {device}")
 
 
-def stream_prefill_init_early(method, layer) -> None:
-    """KT_GPU_STREAM_EARLY_INIT=1: the streamer and every layer's bank at load time."""
+def _streaming_enabled() -> bool:
+    """Streaming is on (KT_GPU_STREAM_PREFILL > 0) and no attempt to build the streamer has
+    failed in this process."""
+    return STREAM_THRESHOLD > 0 and not _failed
+
+
+def _build_streamer(method, layer, occasion: str) -> KTStreamPrefillGGUF:
+    """Makes the process's streamer. Fail-closed: if building it raises, streaming stays off
+    for the rest of the process (the entry points return None from then on) and the error
+    propagates to the caller."""
     global _instance, _failed
-    if not EARLY_INIT or STREAM_THRESHOLD <= 0 or _failed or _instance is not None:
-        return
-    t0 = time.time()
     try:
         _instance = KTStreamPrefillGGUF(method, layer)
-        _instance.build_all_banks()
-    except Exception:
+    except Exception as exc:
         _failed = True
-        _log("early init failed:\n" + traceback.format_exc())
+        _log(f"streaming disabled for this process: building the streamer {occasion} raised "
+             f"{type(exc).__name__}: {exc}")
         raise
-    _log(f"rank {_instance.rank}: streamer built at load time in {time.time() - t0:.0f} s")
+    return _instance
+
+
+def stream_prefill_init_early(method, layer) -> None:
+    """With KT_GPU_STREAM_EARLY_INIT=1, builds the streamer and the pinned bank of every
+    streamed layer while the model loads (the reference's entry point, P:10515), instead of
+    at the first long chunk. Idempotent; a failure disables streaming and propagates."""
+    global _failed
+    if not EARLY_INIT or not _streaming_enabled() or _instance is not None:
+        return
+    started = time.time()
+    st = _build_streamer(method, layer, "at load time")
+    try:
+        st.build_all_banks()
+    except Exception as exc:
+        _failed = True
+        _log(f"streaming disabled for this process: the load-time banks raised {type(exc).__name__}: {exc}")
+        raise
+    _log(f"rank {st.rank}: streamer and banks ready at load time ({time.time() - started:.0f} s)")
 
 
 def stream_prefill_for(method, layer, num_tokens: int) -> Optional[KTStreamPrefillGGUF]:
-    """The streamer for a chunk of num_tokens tokens, or None (streaming off, below the
-    threshold, under graph capture, or after a failed init)."""
-    global _instance, _failed
-    if STREAM_THRESHOLD <= 0 or _failed or num_tokens < STREAM_THRESHOLD:
+    """The streamer that runs a chunk of `num_tokens` tokens (the reference's per-forward
+    entry point, P:10581), or None: streaming off or disabled, a chunk below
+    KT_GPU_STREAM_PREFILL, or a stream under graph capture. The first qualifying chunk
+    builds the streamer."""
+    if not _streaming_enabled() or num_tokens < STREAM_THRESHOLD:
         return None
     if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
         return None
-    if _instance is None:
-        _log(f"first chunk of {num_tokens} tokens (layer {method.kt_config.layer_idx}): building the streamer")
-        try:
-            _instance = KTStreamPrefillGGUF(method, layer)
-        except Exception:
-            _failed = True
-            _log("init failed:\n" + traceback.format_exc())
-            raise
-    return _instance
+    if _instance is not None:
+        return _instance
+    _log(f"building the streamer for a {num_tokens}-token chunk of layer {method.kt_config.layer_idx}")
+    return _build_streamer(method, layer, f"for a {num_tokens}-token chunk")

@@ -65,14 +65,13 @@ def forward(x_bf16: np.ndarray, slot_ids: np.ndarray, weights: np.ndarray, w13: 
 
 
 def default_threads() -> int:
-    """The threads the CPU baseline uses: the cores this process may run on (sched affinity),
-    at most 16 (the CPU share a one-GPU box grants a job; a larger pool would only contend
-    with the other jobs on the host)."""
+    """The threads the CPU baseline uses: the CPUs this process may run on (its sched
+    affinity, which is the share a job scheduler grants), else every logical CPU."""
     try:
         n = len(os.sched_getaffinity(0))
     except AttributeError:
         n = os.cpu_count() or 1
-    return max(1, min(16, n))
+    return max(1, n)
 
 
 def host_info() -> dict:

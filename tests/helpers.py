@@ -64,3 +64,19 @@ def make_expert_gguf(path, layers: int, E: int, N: int, K: int, types, seed: int
                    "toymoe.embedding_length": K})
     G.write_gguf(str(path), md, tensors)
     return raw
+
+
+def scale_f16_fields(rows: np.ndarray, t: int, factor: float) -> np.ndarray:
+    """A copy of GGUF rows uint8 [rows, row_bytes] of type t with every fp16 scale field (d,
+    and Q4_K's dmin) multiplied by `factor`, a power of two >= 1: fp16 products by a power of
+    two are exact (subnormals included) unless they overflow, which is checked, so each
+    dequantised value becomes exactly `factor` times the original."""
+    blck, ts = R.BLOCK_INFO[t]
+    out = np.ascontiguousarray(rows).copy()
+    b = out.reshape(out.shape[0], -1, ts)
+    for off in _F16_FIELDS[t]:
+        h = np.ascontiguousarray(b[:, :, off:off + 2]).view(np.float16)
+        s = (h.astype(np.float32) * np.float32(factor)).astype(np.float16)
+        assert np.all(np.isfinite(s)) and np.array_equal(s.astype(np.float32), h.astype(np.float32) * factor)
+        b[:, :, off:off + 2] = s.view(np.uint8)
+    return out

@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 
 from conftest import bf16_bits_of, bf16_tensor, to_dev
-from helpers import dequant_w
+from helpers import dequant_w, scale_f16_fields
 from oracle import gguf_ref as R
 
 pytestmark = pytest.mark.gpu
@@ -92,8 +92,11 @@ def test_iq3_s_16k_chunk(dev):
 
 class _MemExperts:
     """An expert source over pinned host banks (the streamer's reader interface: E, inter, K,
-    layers(), types(l), banks(l, N, rank, p2l)); bank row e of layer l holds distinct
-    expert (e + l) % D, so every layer routes to a different arrangement."""
+    layers(), types(l), banks(l, N, rank, p2l)). Bank row e of layer l is distinct expert
+    (e + l) % D with a signature of its own: the fp16 scales of its gate rows and of its
+    down rows multiplied by 2^(e // D) (an exact scaling of their dequantised values), so no
+    two rows of a layer hold the same bytes and a slot or row read from the wrong place
+    changes the output."""
 
     def __init__(self, w, D, layers):
         import torch
@@ -107,11 +110,33 @@ class _MemExperts:
         N = w.inter
         self._banks = {}
         for li in range(layers):
-            rows = [(e + li) % D for e in range(self.E)]
-            gate = torch.from_numpy(np.stack([self.parts[r][0][:N].reshape(-1) for r in rows])).pin_memory()
-            up = torch.from_numpy(np.stack([self.parts[r][0][N:].reshape(-1) for r in rows])).pin_memory()
-            down = torch.from_numpy(np.stack([self.parts[r][1].reshape(-1) for r in rows])).pin_memory()
-            self._banks[li] = [gate, up, down]
+            gate, up, down = [], [], []
+            for e in range(self.E):
+                w13, w2 = self.parts[self.base(li, e)]
+                f = self.factor(e)
+                gate.append(scale_f16_fields(w13[:N], w.types[0], f).reshape(-1))
+                up.append(w13[N:].reshape(-1))
+                down.append(scale_f16_fields(w2, w.types[2], f).reshape(-1))
+            self._banks[li] = [torch.from_numpy(np.stack(p)).pin_memory() for p in (gate, up, down)]
+
+    def base(self, layer_idx, e):
+        return (e + layer_idx) % self.D
+
+    def factor(self, e):
+        return float(2 ** (e // self.D))
+
+    def reference(self, layer_idx, xb, slot, tw, g, d):
+        """The oracle's FFN over bank rows: row e's weights are its base expert's dequantised
+        values with the gate rows and the down rows times factor(e), one row at a time."""
+        N = self.inter
+        ref = np.zeros((xb.shape[0], self.K), np.float64)
+        for e in np.unique(slot[slot >= 0]):
+            b, f = self.base(layer_idx, int(e)), np.float32(self.factor(int(e)))
+            ge = g[b].copy()
+            ge[:N] *= f
+            ids = np.where(slot == e, 0, -1).astype(np.int32)
+            ref += R.ffn_reference(xb, ids, tw, ge[None], (d[b] * f)[None])
+        return ref
 
     def layers(self):
         return list(range(self.num_layers))
@@ -131,7 +156,8 @@ def test_streamed_large_expert_layers(dev, monkeypatch):
     (method, layer, T) and run(method, layer, dispatch_output, physical_ids), groups of 8
     experts in the two slots. Each layer against the oracle's FFN on a token sample; the
     4-layer pipeline (run_layers) equal to the per-layer runs bit for bit; one group of all
-    24 experts equal to the resident layer bit for bit."""
+    24 experts equal to the resident layer bit for bit. Every bank row carries its own
+    signature (_MemExperts), so each slot's bytes are checked where they land."""
     from types import SimpleNamespace as NS
 
     import torch
@@ -173,8 +199,7 @@ def test_streamed_large_expert_layers(dev, monkeypatch):
         torch.cuda.synchronize()
         got = R.bf16_to_f32(bf16_bits_of(y))
         outs.append(bf16_bits_of(y))
-        mapped = np.where(slot >= 0, (slot + li) % D, -1).astype(np.int32)
-        ref = R.ffn_reference(xb[sample], mapped[sample], tw[sample], g, d)
+        ref = src.reference(li, xb[sample], slot[sample], tw[sample], g, d)
         l2, l1, cos = R.rel_errors(got[sample], ref)
         print(f"config 5 layer {li}: rel L2 {l2:.2e} rel L1 {l1:.2e} cos {cos:.6f}", flush=True)
         assert l2 < TOL_REL_L2 and cos > 0.999, (li, l2, l1, cos)

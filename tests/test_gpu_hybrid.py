@@ -102,3 +102,47 @@ def test_hot_split_apply_with_cpu_engine(dev):
     l2, _, cos = R.rel_errors(R.bf16_to_f32(bf16_bits_of(y)), R.ffn_reference(xb, ids, w, g, d))
     assert l2 < TOL_REL_L2 and cos > 0.999, (l2, cos)
     cpu.close()
+
+
+def test_add_gives_up_past_its_bound(dev):
+    """A decode window whose CPU side takes longer than the add's wait bound (forced from the
+    host: a 200 us bound, one CPU thread, 256 tokens of cold routes): every block of the add
+    stops waiting and exits normally, the layer's rows become NaN, sync_add raises, and the
+    engine serves the next layer correctly with the default bound."""
+    import torch
+
+    import kt_prefill_lend_amd.kt_cpu_moe as CM
+
+    w13, w2, cpu8, _ = _setup(dev)
+    cpu8.close()
+    bank = [torch.from_numpy(np.ascontiguousarray(w13[:, :N].reshape(E, -1))).pin_memory(),
+            torch.from_numpy(np.ascontiguousarray(w13[:, N:].reshape(E, -1))).pin_memory(),
+            torch.from_numpy(np.ascontiguousarray(w2.reshape(E, -1))).pin_memory()]
+    cpu = CM.KTCPUExperts(*bank, K, N, TYPES, threads=1, max_tokens=256, max_top_k=TOPK)
+    T = 256
+    ids, w = _routes(T, 77)
+    xb = R.bf16_bits(np.random.default_rng(77).standard_normal((T, K)).astype(np.float32))
+    x, wd, ids_d = bf16_tensor(xb, dev), to_dev(w, dev), to_dev(ids, dev)
+    t0 = __import__("time").perf_counter()
+    cpu.forward(torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16), torch.from_numpy(ids), torch.from_numpy(w))
+    cpu_ms = (__import__("time").perf_counter() - t0) * 1e3
+    assert cpu_ms > 1.0, cpu_ms  # the CPU side outlasts the bound by a wide margin
+    cpu.set_add_wait(200)
+    y = torch.zeros((T, K), dtype=torch.bfloat16, device=dev)
+    cpu.submit(x, ids_d, wd)
+    with pytest.raises(RuntimeError, match="stopped waiting"):
+        cpu.sync_add(y)
+    torch.cuda.synchronize()
+    assert torch.isnan(y.float()).all()
+    cpu.set_add_wait(10_000_000)
+    y = torch.zeros((T, K), dtype=torch.bfloat16, device=dev)
+    cpu.submit(x, ids_d, wd)
+    cpu.sync_add(y)
+    torch.cuda.synchronize()
+    y_cpu = cpu.forward(torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16), torch.from_numpy(ids),
+                        torch.from_numpy(w))
+    # out starts at zero: the add gives bf16(0 + cpu) (+0 where the CPU side gave -0)
+    assert np.array_equal(bf16_bits_of(y), R.bf16_bits(R.bf16_to_f32(bf16_bits_of(y_cpu)) + np.float32(0)))
+    with pytest.raises(RuntimeError):
+        cpu.set_add_wait(0)
+    cpu.close()

@@ -198,3 +198,33 @@ def test_combine_bit_exact(dev):
     got = bf16_bits_of(H._combine(bf16_tensor(ob, dev).view(T, k, K), to_dev(w, dev)))
     torch.cuda.synchronize()
     assert np.array_equal(got, R.combine(ob, w))
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("tokens", [2, 4])
+def test_dense_a8_vec(dev, t, tokens):
+    """dense_a8_vec (hot/kt_gguf_moe_multi.py:98-112): a dense GGUF linear of 520 rows (past
+    DENSE_MIN_ROWS, not a multiple of 32) run as a one-expert MoE. Its rows are the MoE GEMV's
+    with every token on expert 0, bit for bit, and the oracle's literal vec_dot sums within
+    the GEMV tests' bound."""
+    import torch
+
+    _, M, _, _ = _pkg()
+    rng = np.random.default_rng(300 + 7 * t + tokens)
+    rows = 520
+    cols = 768 if t == R.GGML_Q8_0 else 512
+    Wn = random_blocks(t, rows, cols, rng)
+    W = to_dev(Wn, dev)
+    xb = R.bf16_bits(rng.standard_normal((tokens, cols)).astype(np.float32))
+    x = bf16_tensor(xb, dev)
+    assert M.dense_ok(x, W, t)
+    y = M.dense_a8_vec(x, W, t)
+    zeros = torch.zeros(tokens, dtype=torch.int32, device=dev)
+    y_moe = M.moe_a8_vec_multi(x, W.view(1, rows, -1), zeros, 1, t, rows, tokens)
+    torch.cuda.synchronize()
+    assert y.shape == (tokens, rows) and torch.equal(y, y_moe.view(tokens, rows))
+    got = y.float().cpu().numpy()
+    ref = R.moe_a8_vec(R.bf16_to_f32(xb), Wn[None], np.zeros(tokens, np.int32), 1, t, rows, tokens)
+    scale = np.abs(ref).max()
+    assert np.abs(got - ref).max() <= 1e-2 * scale + 1e-6, (np.abs(got - ref).max(), scale)
+    assert R.rel_errors(got, ref)[0] < 5e-3

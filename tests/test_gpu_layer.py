@@ -172,6 +172,30 @@ def test_grouped_past_the_combine_grid_limit(dev):
     assert l2 < TOL_REL_L2 and cos > 0.999, (l2, l1, cos)
 
 
+@pytest.mark.timeout(300)
+def test_grouped_past_one_pass(dev):
+    """Hidden 7168, top-8: a grouped pass holds 37376 tokens (its Y buffer [R, hidden] bf16
+    stays under the kernels' 32-bit offsets), so 37676 tokens run as two passes. The tokens
+    of the second pass equal a call on those tokens alone, bit for bit, and a token sample
+    from both passes, around the boundary included, matches the fp64 FFN."""
+    L, H, _ = _pkg()
+    w, xb, tw, slot, w13, w2 = _case("q4_k+q6_k-h2048-n512-e256-k8-hot40-prefill", 37676, 7168, 256, 4, 32)
+    desc = L.ktmi_layer(hidden=w.hidden, inter=w.inter, n_slots=w.hot, type13=w.types[0], type2=w.types[2],
+                        w13=1 << 20, w2=1 << 21)
+    cut = L.lib().ktmi_moe_layer_pass_tokens(desc, w.top_k)
+    T = xb.shape[0]
+    assert cut == 37376 and T > cut
+    print(f"past one pass: {T} tokens, {(slot >= 0).sum()} hot routes", flush=True)
+    y = _run(dev, w, xb, tw, slot, w13, w2, L.MODE_GROUPED)
+    tail = _run(dev, w, xb[cut:], tw[cut:], slot[cut:], w13, w2, L.MODE_GROUPED)
+    assert np.array_equal(y[cut:], tail)
+    g, d = dequant_w(w13, w2, w.types, w.hidden, w.inter)
+    sample = np.concatenate([np.arange(0, cut - 8, 997), np.arange(cut - 8, T, 31)])
+    ref = R.ffn_reference(xb[sample], slot[sample], tw[sample], g, d)
+    l2, l1, cos = R.rel_errors(R.bf16_to_f32(y[sample]), ref)
+    assert l2 < TOL_REL_L2 and cos > 0.999, (l2, l1, cos)
+
+
 def test_grouped_at_full_shape(dev):
     """The prefill workload's real layer shape (hidden 2048, inter 512, 40 slots, Q4_K/Q6_K)
     at 1024 tokens, against the fp64 FFN on a sample of tokens."""

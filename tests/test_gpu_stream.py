@@ -145,3 +145,37 @@ def test_streamer_rejects_bad_groups(dev):
     with pytest.raises(RuntimeError, match="experts"):
         st._stage(0, 0, 4, 4)
     st.close()
+
+
+def test_selftest_logs_agreement(dev, monkeypatch, capsys):
+    """KT_GPU_STREAM_SELFTEST=2 (P:40821-40853, called at P:40986-40987): the first streamed
+    layer's run() recomputes the streamed experts' share in fp32 and logs the agreement;
+    the logged relative L2 is below the 2e-2 bar, and the same check on a damaged output
+    reports the damage (it is not vacuous)."""
+    import re
+    from types import SimpleNamespace as NS
+
+    import torch
+
+    L, H, SP, _ = _pkg()
+    (wl, xb, tw, slot, w13, w2), = _layers(1, 40)
+    monkeypatch.setattr(SP, "SELFTEST", "2")
+    st = SP.KTStreamPrefillGGUF.standalone(wl.inter, wl.hidden, wl.top_k, wl.types, group_size=4, device=dev)
+    st.set_bank(0, SP.Bank.from_slot_rows(torch.from_numpy(w13), torch.from_numpy(w2), wl.inter, wl.types))
+    x, tw_d, ids_d = bf16_tensor(xb, dev), to_dev(tw, dev), to_dev(slot, dev)
+    method = NS(kt_config=NS(layer_idx=0), num_gpu_experts=0, gpu_method=NS(streams_hot_experts=True))
+    do = H.DispatchOutput(x, H.TopKOutput(tw_d, ids_d, None))
+    acc = st.run(method, None, do, ids_d)
+    torch.cuda.synchronize()
+    log = capsys.readouterr().out
+    m = re.search(r"self-check of layer 0 .*rel L2 (\S+), cos (\S+)", log)
+    assert m, log
+    rel, cos = float(m.group(1)), float(m.group(2))
+    assert rel < 2e-2 and cos > 0.999, log
+    # once per process: a second run does not check again
+    st.run(method, None, do, ids_d)
+    torch.cuda.synchronize()
+    assert "self-check" not in capsys.readouterr().out
+    rel_bad, _ = st._reference_check(0, x, ids_d, tw_d, acc * 0.5, 0)
+    assert 0.45 < rel_bad < 0.55, rel_bad
+    st.close()

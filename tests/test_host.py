@@ -369,8 +369,7 @@ def test_sglang_expert_location_map_places_the_slots(monkeypatch):
 def test_layer_argument_errors_before_device_work():
     """The layer entry point rejects bad arguments with a status and a message before it
     touches the device (the pointers below are never dereferenced): a short workspace,
-    misaligned activations, a forced GEMV mode past its route limit, a chunk past the
-    activations' 4 GiB buffer range."""
+    misaligned activations, a forced GEMV mode past its route limit."""
     from kt_prefill_lend_amd import _lib
 
     L = _lib.lib()
@@ -383,5 +382,70 @@ def test_layer_argument_errors_before_device_work():
     assert rc == -1 and b"aligned" in L.ktmi_last_error()
     rc = L.ktmi_moe_layer(d, p, p, p, 10000, 8, p, p, big, _lib.MODE_GEMV, 0)
     assert rc == -1 and b"65535" in L.ktmi_last_error()
-    rc = L.ktmi_moe_layer(d, p, p, p, 1 << 20, 8, p, p, big, _lib.MODE_GROUPED, 0)
-    assert rc == -1 and b"4 GiB" in L.ktmi_last_error()
+
+
+@pytest.mark.parametrize("hidden,inter,top_k,pass_tokens", [(7168, 2048, 8, 37376), (2048, 512, 8, 130816),
+                                                             (512, 4096, 10, 52224), (256, 256, 1, 8388352)])
+def test_grouped_pass_plan(hidden, inter, top_k, pass_tokens):
+    """The grouped mode's token passes: the largest multiple of 256 tokens whose x [T, hidden],
+    H [T top_k, inter] and Y [T top_k, hidden] bf16 buffers all stay under 4 GiB - 64 KiB (its
+    kernels' 32-bit buffer offsets, 0xFFFFFFF0 marking a dropped store); the workspace covers
+    one pass, so it grows with the tokens up to a pass and stays there."""
+    from kt_prefill_lend_amd import _lib
+
+    L = _lib.lib()
+    d = _lib.ktmi_layer(hidden=hidden, inter=inter, n_slots=24, type13=12, type2=14, w13=1 << 20, w2=2 << 20)
+    got = L.ktmi_moe_layer_pass_tokens(d, top_k)
+    assert got == pass_tokens
+    limit = 0xFFFF0000
+    assert 2 * got * hidden <= limit and 2 * got * top_k * inter <= limit and 2 * got * top_k * hidden <= limit
+    nxt = got + 256
+    assert max(2 * nxt * top_k * inter, 2 * nxt * top_k * hidden) > limit
+    ws = lambda t: L.ktmi_moe_layer_workspace(d, t, top_k, _lib.MODE_GROUPED)  # noqa: E731
+    assert ws(got - 1) < ws(got) == ws(got + 1) == ws(3 * got + 17)
+    # the Y buffer of one pass alone is R * hidden * 2 bytes
+    assert ws(got) >= 2 * got * top_k * hidden
+
+
+def test_dense_ok_and_reads_table(monkeypatch):
+    """dense_ok / reads_table (hot/kt_gguf_moe_multi.py:90-100): the dense GEMV takes 2 to
+    KT_GGUF_MOE_MAXM tokens of a contiguous uint8 weight with more than 512 rows of a type with
+    kernels, unless KT_GGUF_DENSE_MULTI=0; every ktmi kernel reads slot weights through the
+    pointer table, so reads_table only follows KT_GGUF_MOE_MULTI."""
+    import torch
+
+    import kt_prefill_lend_amd.kt_gguf_moe_multi as M
+
+    x = lambda t: torch.zeros((t, 512), dtype=torch.bfloat16)  # noqa: E731
+    w = lambda r: torch.zeros((r, 288), dtype=torch.uint8)  # noqa: E731
+    assert M.MAX_TOKENS == 4 and M.DENSE_MIN_ROWS == 513
+    assert M.dense_ok(x(2), w(513), 12) and M.dense_ok(x(4), w(4096), 14)
+    assert not M.dense_ok(x(1), w(513), 12)   # one token: the plain GEMV
+    assert not M.dense_ok(x(5), w(513), 12)   # past the window
+    assert not M.dense_ok(x(2), w(512), 12)   # small matrices stay on the plain path
+    assert not M.dense_ok(x(2), w(513), 13)   # Q5_K: no kernel here
+    assert not M.dense_ok(x(2), w(600)[:, :144].contiguous().t(), 12)  # not [rows, bytes] contiguous
+    assert not M.dense_ok(x(2), w(1024)[::2], 12)
+    assert not M.dense_ok(x(2), torch.zeros((513, 72), dtype=torch.int32), 12)
+    monkeypatch.setattr(M, "DENSE", False)
+    assert not M.dense_ok(x(2), w(513), 12)
+    for t in (1, 4, 5, 64):
+        assert M.reads_table(t)
+    monkeypatch.setenv("KT_GGUF_MOE_MULTI", "0")
+    assert not M.reads_table(1)
+
+
+def test_scale_f16_fields_scales_dequant_exactly():
+    """The test helper that signs bank rows: fp16 scales times a power of two give exactly
+    that multiple of every dequantised value (so the oracle can scale its arrays instead of
+    decoding the signed rows)."""
+    from helpers import TYPES, random_blocks, scale_f16_fields
+    from oracle import gguf_ref as R
+
+    rng = np.random.default_rng(4)
+    for t in TYPES:
+        cols = 512
+        rows = random_blocks(t, 6, cols, rng)
+        for f in (2.0, 128.0):
+            got = R.dequant_rows(scale_f16_fields(rows, t, f), t, cols)
+            assert np.array_equal(got, R.dequant_rows(rows, t, cols) * np.float32(f)), (t, f)
