@@ -35,8 +35,14 @@ extern "C" {
 
 /* layer modes for ktmi_moe_layer */
 #define KTMI_MODE_AUTO 0
-#define KTMI_MODE_GEMV 1    /* decode windows: int8 dot-product GEMV over raw blocks */
-#define KTMI_MODE_GROUPED 2 /* prefill chunks: routes sorted by slot, dequant-in-LDS bf16 MFMA */
+#define KTMI_MODE_GEMV 1    /* decode windows: int8 dot-product GEMV over raw blocks and q8_1
+                               activations (the reference kernels' numerics) */
+#define KTMI_MODE_GROUPED 2 /* prefill chunks: routes sorted by slot, weights dequantised into
+                               bf16 MFMA operands */
+#define KTMI_MODE_DECODE 3  /* decode windows (at most 256 routes of 64 tokens): weights
+                               dequantised into bf16 MFMA operands, a slot's routes as the
+                               matrix columns, fp32 sums (within the layer tolerance of the
+                               GEMV mode, not bit-equal to it) */
 
 /* Thread-local text of the last failure ("" if none). */
 const char* ktmi_last_error(void);
@@ -129,7 +135,8 @@ int64_t ktmi_moe_layer_workspace(const ktmi_layer* layer, int64_t tokens, int64_
 int ktmi_moe_layer(const ktmi_layer* layer, const void* x, const float* topk_w, const int32_t* slot_ids,
                    int64_t tokens, int64_t top_k, void* y, void* workspace, int64_t ws_bytes, int mode,
                    void* stream);
-/* The mode KTMI_MODE_AUTO picks for this many routes. */
+/* The mode KTMI_MODE_AUTO picks for this many routes: GROUPED above 256 routes, else DECODE
+ * where it applies, else GEMV. */
 int ktmi_moe_layer_mode(const ktmi_layer* layer, int64_t tokens, int64_t top_k);
 /* Tokens per pass of KTMI_MODE_GROUPED: a longer call runs as consecutive passes over token
  * slices of this size (each token's output depends only on its own routes), and the

@@ -14,7 +14,7 @@ LIB_PATH = Path(os.environ.get("KTMI_LIB", Path(__file__).resolve().parent / "li
 
 KTMI_OK = 0
 KTMI_F32, KTMI_F16, KTMI_BF16 = 0, 1, 2
-MODE_AUTO, MODE_GEMV, MODE_GROUPED = 0, 1, 2
+MODE_AUTO, MODE_GEMV, MODE_GROUPED, MODE_DECODE = 0, 1, 2, 3
 STAGE_EVENTS = 6
 NOALLOC_SCRATCH_BYTES = 64 << 20  # KTMI_NOALLOC_SCRATCH_BYTES
 

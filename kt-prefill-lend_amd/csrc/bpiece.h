@@ -24,6 +24,12 @@
 //   Q8_0, IQ3_S: positions [32h, 32h+32) (one Q8_0 block, one IQ3_S 32-group)
 // `off0`/`off1` give the step positions of out[0..7] and out[8..15] (16 values each).
 //
+// Every SUB-dependent member also exists with the step parity as a run-time value: the
+// `_hp<S2>(..., p)` forms take SUB = 2 S2 + p with S2 a compile-time constant and p a
+// per-lane value (the decode-sized layer's 16x16x32 MFMA operands hold pieces of both
+// parities in one wave); the `<SUB>` forms are those with p constant. One body per format
+// serves both, so the values are the same.
+//
 // 2-byte aligned blocks (Q8_0 34 B, Q6_K 210 B, IQ3_S 110 B) are read with dword loads
 // from the dword-aligned address below and realigned with v_alignbyte; every dword read
 // holds at least one byte of the block, so no load leaves the tensor's pages.
@@ -55,6 +61,17 @@ __device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
   return r;
 }
 
+// Where a piece's bytes are read from: global memory (through the caches) or LDS (rows a
+// kernel has staged there, at the same offsets as in the row).
+struct GMem {
+  template <typename T>
+  __device__ __forceinline__ static T ld(const void* p) { return gload<T>(p); }
+};
+struct LMem {
+  template <typename T>
+  __device__ __forceinline__ static T ld(const void* p) { return *(const __attribute__((address_space(3))) T*)p; }
+};
+
 template <int TYPE>
 struct BPiece;
 
@@ -70,6 +87,22 @@ struct NoLookup {
   __device__ static void convert(const Head& hd, const Raw& r, const uint32_t* grid, const Look&, uint32_t out[16]) {
     P::template decode<SUB>(hd, r, grid, out);
   }
+  template <int S2, class Head, class Raw>
+  __device__ static void lookup_hp(const Head&, const Raw&, const uint32_t*, int, Look&) {}
+  template <int S2, class Head, class Raw>
+  __device__ static void convert_hp(const Head& hd, const Raw& r, const uint32_t* grid, int p, const Look&,
+                                    uint32_t out[16]) {
+    P::template decode_hp<S2>(hd, r, grid, p, out);
+  }
+  // the <SUB> forms through the run-time parity bodies
+  template <int SUB, class Raw>
+  __device__ static void load(const uint8_t* row, int sb, int h, const uint32_t* grid, Raw& r) {
+    P::template load_hp<SUB / 2>(row, sb, h, SUB & 1, grid, r);
+  }
+  template <int SUB, class Head, class Raw>
+  __device__ static void decode(const Head& hd, const Raw& r, const uint32_t* grid, uint32_t out[16]) {
+    P::template decode_hp<SUB / 2>(hd, r, grid, SUB & 1, out);
+  }
 };
 
 template <>
@@ -80,21 +113,26 @@ struct BPiece<GGML_Q4_K> : NoLookup<BPiece<GGML_Q4_K>> {
   struct Raw { u32x4_t q; };
   template <int SUB>
   __device__ static int ksub() { return 64 * SUB; }
+  template <int S2>
+  __device__ static int ksub_hp(int p) { return 128 * S2 + 64 * p; }
   __device__ static int coff(int q) { return 8 * q; }
-  __device__ static void load_head(const uint8_t* row, int sb, int, Head& hd) { hd.hdr = gload<u32x4_t>(row + sb * QB4_K); }
-  template <int SUB>
-  __device__ static void load(const uint8_t* row, int sb, int h, const uint32_t*, Raw& r) {
-    r.q = gload<u32x4_t>(row + sb * QB4_K + 16 + 32 * SUB + 16 * h);
+  template <class M = GMem>
+  __device__ static void load_head(const uint8_t* row, int sb, int, Head& hd) { hd.hdr = M::template ld<u32x4_t>(row + sb * QB4_K); }
+  template <int S2, class M = GMem>
+  __device__ __forceinline__ static void load_hp(const uint8_t* row, int sb, int h, int p, const uint32_t*, Raw& r) {
+    r.q = M::template ld<u32x4_t>(row + sb * QB4_K + 16 + 64 * S2 + 32 * p + 16 * h);
   }
-  template <int SUB>
-  __device__ static void decode(const Head& hd, const Raw& r, const uint32_t*, uint32_t out[16]) {
+  template <int S2>
+  __device__ __forceinline__ static void decode_hp(const Head& hd, const Raw& r, const uint32_t*, int p,
+                                                   uint32_t out[16]) {
     const float d = half_bits_to_float(hd.hdr[0] & 0xFFFF);
     const float dmin = half_bits_to_float(hd.hdr[0] >> 16);
-    // sub-blocks 2g, 2g+1: for g < 2 the 6-bit fields sit in scales[0..7]; for g >= 2 the
-    // low 4 bits are in scales[8..11] and the high 2 bits in bits 6-7 of scales[0..7]
-    constexpr int sh = 16 * (SUB & 1);
+    // sub-blocks 2g, 2g+1 (g = SUB = 2 S2 + p): for g < 2 the 6-bit fields sit in
+    // scales[0..7]; for g >= 2 the low 4 bits are in scales[8..11] and the high 2 bits in
+    // bits 6-7 of scales[0..7]
+    const int sh = 16 * p;
     const uint32_t ws = hd.hdr[1] >> sh, wm = hd.hdr[2] >> sh, lo = hd.hdr[3] >> sh;
-    constexpr bool hi = SUB >= 2;
+    constexpr bool hi = S2 == 1;
     const int sc0 = hi ? (int)((lo & 15) | (((ws >> 6) & 3) << 4)) : (int)(ws & 63);
     const int sc1 = hi ? (int)(((lo >> 8) & 15) | (((ws >> 14) & 3) << 4)) : (int)((ws >> 8) & 63);
     const int m0 = hi ? (int)(((lo >> 4) & 15) | (((wm >> 6) & 3) << 4)) : (int)(wm & 63);
@@ -124,23 +162,26 @@ struct BPiece<GGML_Q8_0> : NoLookup<BPiece<GGML_Q8_0>> {
   struct Raw { uint32_t w[9]; uint32_t s; };
   template <int SUB>
   __device__ static int ksub() { return 64 * SUB; }
+  template <int S2>
+  __device__ static int ksub_hp(int p) { return 128 * S2 + 64 * p; }
   __device__ static int coff(int q) { return 8 * q; }
+  template <class M = GMem>
   __device__ static void load_head(const uint8_t*, int, int, Head&) {}
-  template <int SUB>
-  __device__ static void load(const uint8_t* row, int sb, int h, const uint32_t*, Raw& r) {
-    const uint8_t* b = row + (8 * sb + 2 * SUB + h) * QB8_0;
+  template <int S2, class M = GMem>
+  __device__ __forceinline__ static void load_hp(const uint8_t* row, int sb, int h, int p, const uint32_t*, Raw& r) {
+    const uint8_t* b = row + (8 * sb + 4 * S2 + 2 * p + h) * QB8_0;
     const uint32_t* a = dword_floor(b);
     r.s = byte_shift(b);  // 0 or 2
-    const u32x4_t w0 = gload<u32x4_a4_t>(a), w1 = gload<u32x4_a4_t>(a + 4);
+    const u32x4_t w0 = M::template ld<u32x4_a4_t>(a), w1 = M::template ld<u32x4_a4_t>(a + 4);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       r.w[i] = w0[i];
       r.w[4 + i] = w1[i];
     }
-    r.w[8] = gload<uint32_t>(a + 8);
+    r.w[8] = M::template ld<uint32_t>(a + 8);
   }
-  template <int SUB>
-  __device__ static void decode(const Head&, const Raw& r, const uint32_t*, uint32_t out[16]) {
+  template <int S2>
+  __device__ __forceinline__ static void decode_hp(const Head&, const Raw& r, const uint32_t*, int, uint32_t out[16]) {
     const float d = half_bits_to_float(r.s ? (r.w[0] >> 16) : (r.w[0] & 0xFFFF));
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -164,35 +205,41 @@ struct BPiece<GGML_Q6_K> : NoLookup<BPiece<GGML_Q6_K>> {
   struct Raw { uint32_t ql[5], qh[5]; };
   template <int SUB>
   __device__ static int ksub() { return 128 * (SUB >> 1) + 32 * (SUB & 1); }
+  template <int S2>
+  __device__ static int ksub_hp(int p) { return 128 * S2 + 32 * p; }
   __device__ static int coff(int q) { return q < 4 ? 8 * q : 64 + 8 * (q - 4); }
+  template <class M = GMem>
   __device__ static void load_head(const uint8_t* row, int sb, int, Head& hd) {
     const uint8_t* sc = row + sb * QB6_K + 192;
     hd.s = byte_shift(sc);
     const uint32_t* a = dword_floor(sc);
-    const u32x4_t w = gload<u32x4_a4_t>(a);
+    const u32x4_t w = M::template ld<u32x4_a4_t>(a);
 #pragma unroll
     for (int i = 0; i < 4; ++i) hd.w[i] = w[i];
-    hd.w[4] = gload<uint32_t>(a + 4);
+    hd.w[4] = M::template ld<uint32_t>(a + 4);
   }
-  template <int SUB>
-  __device__ static void load(const uint8_t* row, int sb, int h, const uint32_t*, Raw& r) {
+  template <int S2, class M = GMem>
+  __device__ __forceinline__ static void load_hp(const uint8_t* row, int sb, int h, int p, const uint32_t*, Raw& r) {
     const uint8_t* b = row + sb * QB6_K;
-    constexpr int hh = SUB >> 1, c = SUB & 1;
+    constexpr int hh = S2;
+    const int c = p;
     const uint32_t* ql = dword_floor(b + 64 * hh + 32 * c + 16 * h);
     const uint32_t* qh = dword_floor(b + 128 + 32 * hh + 16 * h);
     // 16 bytes each from the dword below them: one dwordx4 and the dword after it
-    const u32x4_t l4 = gload<u32x4_a4_t>(ql), h4 = gload<u32x4_a4_t>(qh);
+    const u32x4_t l4 = M::template ld<u32x4_a4_t>(ql), h4 = M::template ld<u32x4_a4_t>(qh);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       r.ql[i] = l4[i];
       r.qh[i] = h4[i];
     }
-    r.ql[4] = gload<uint32_t>(ql + 4);
-    r.qh[4] = gload<uint32_t>(qh + 4);
+    r.ql[4] = M::template ld<uint32_t>(ql + 4);
+    r.qh[4] = M::template ld<uint32_t>(qh + 4);
   }
-  template <int SUB>
-  __device__ static void decode(const Head& hd, const Raw& r, const uint32_t*, uint32_t out[16]) {
-    constexpr int hh = SUB >> 1, c = SUB & 1;
+  template <int S2>
+  __device__ __forceinline__ static void decode_hp(const Head& hd, const Raw& r, const uint32_t*, int p,
+                                                   uint32_t out[16]) {
+    constexpr int hh = S2;
+    const int c = p;
     const uint32_t s = hd.s;  // the same shift as the block start (192 = 0 mod 4)
     // scales[8hh + 2c + h] (run c) and scales[8hh + 2c + h + 4] (run c+2): bytes 2c + h of
     // the realigned scale words 2hh and 2hh + 1
@@ -208,14 +255,14 @@ struct BPiece<GGML_Q6_K> : NoLookup<BPiece<GGML_Q6_K>> {
     // both runs' codes; the code then sits in bits 2..7 of its byte.
     const float d1a = 0.25f * (d * (float)(int8_t)((sa >> (16 * c + h8)) & 0xFF));
     const float d1b = 0.25f * (d * (float)(int8_t)((sbw >> (16 * c + h8)) & 0xFF));
-    constexpr int hsh = 2 * c;
+    const int hsh = 2 * c;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t lw = alignbyte(r.ql[i + 1], r.ql[i], s);
       const uint32_t hw = alignbyte(r.qh[i + 1], r.qh[i], s) ^ 0xAAAAAAAAu;
       // run c: low nibbles and qh bits hsh, hsh+1; run c+2: high nibbles and bits hsh+4, hsh+5
       const uint32_t va = bfi(0xC0C0C0C0u, hw << (6 - hsh), (lw & 0x0F0F0F0Fu) << 2);
-      const uint32_t vb = bfi(0xC0C0C0C0u, hsh == 2 ? hw : hw << 2, (lw >> 2) & 0x3C3C3C3Cu);
+      const uint32_t vb = bfi(0xC0C0C0C0u, hw << (2 - hsh), (lw >> 2) & 0x3C3C3C3Cu);
       out[2 * i] = f2bf2(d1a * (float)(int8_t)(va & 0xFF), d1a * (float)(int8_t)((va >> 8) & 0xFF));
       out[2 * i + 1] = f2bf2(d1a * (float)(int8_t)((va >> 16) & 0xFF), d1a * (float)(int8_t)(va >> 24));
       out[8 + 2 * i] = f2bf2(d1b * (float)(int8_t)(vb & 0xFF), d1b * (float)(int8_t)((vb >> 8) & 0xFF));
@@ -238,35 +285,39 @@ struct BPiece<GGML_IQ3_S> {
   struct Raw { uint32_t qs[3], sg[2], qh; };
   template <int SUB>
   __device__ static int ksub() { return 64 * SUB; }
+  template <int S2>
+  __device__ static int ksub_hp(int p) { return 128 * S2 + 64 * p; }
   __device__ static int coff(int q) { return 8 * q; }
+  template <class M = GMem>
   __device__ static void load_head(const uint8_t* row, int sb, int, Head& hd) {
     const uint8_t* b = row + sb * QBIQ3_S;
     hd.s = byte_shift(b);
-    hd.dw = gload<uint32_t>(dword_floor(b));
-    hd.sc0 = gload<uint32_t>(dword_floor(b + 106));
-    hd.sc1 = gload<uint32_t>(dword_floor(b + 108));
+    hd.dw = M::template ld<uint32_t>(dword_floor(b));
+    hd.sc0 = M::template ld<uint32_t>(dword_floor(b + 106));
+    hd.sc1 = M::template ld<uint32_t>(dword_floor(b + 108));
   }
-  template <int SUB>
-  __device__ static void load(const uint8_t* row, int sb, int h, const uint32_t*, Raw& r) {
+  template <int S2, class M = GMem>
+  __device__ __forceinline__ static void load_hp(const uint8_t* row, int sb, int h, int p, const uint32_t*, Raw& r) {
     const uint8_t* b = row + sb * QBIQ3_S;
-    const int ib = 2 * SUB + h;
+    const int ib = 4 * S2 + 2 * p + h;
     const uint32_t* q = dword_floor(b + 2 + 8 * ib);
-    const u32x2_t q2 = gload<u32x2_a4_t>(q);
+    const u32x2_t q2 = M::template ld<u32x2_a4_t>(q);
     r.qs[0] = q2[0];
     r.qs[1] = q2[1];
-    r.qs[2] = gload<uint32_t>(q + 2);
-    const u32x2_t s2 = gload<u32x2_a4_t>(dword_floor(b + 74 + 4 * ib));
+    r.qs[2] = M::template ld<uint32_t>(q + 2);
+    const u32x2_t s2 = M::template ld<u32x2_a4_t>(dword_floor(b + 74 + 4 * ib));
     r.sg[0] = s2[0];
     r.sg[1] = s2[1];
-    r.qh = gload<uint32_t>(dword_floor(b + 66 + ib));
+    r.qh = M::template ld<uint32_t>(dword_floor(b + 66 + ib));
   }
   // the 8 codebook entries of the piece's 4-value groups
   struct Look { uint32_t g[8]; };
-  template <int SUB>
-  __device__ static void lookup(const Head& hd, const Raw& r, const uint32_t* grid, Look& lk) {
+  template <int S2>
+  __device__ __forceinline__ static void lookup_hp(const Head& hd, const Raw& r, const uint32_t* grid, int p,
+                                                   Look& lk) {
     const uint32_t s = hd.s;
     const uint32_t h = (threadIdx.x >> 5) & 1;
-    const int ib = 2 * SUB + (int)h;
+    const int ib = 4 * S2 + 2 * p + (int)h;
     // block byte offsets: qs at 2 + 8 ib (= s + 2 mod 4), qh at 66 + ib
     const uint32_t s2 = (s + 2) & 3;
     const uint32_t qs0 = alignbyte(r.qs[1], r.qs[0], s2), qs1 = alignbyte(r.qs[2], r.qs[1], s2);
@@ -277,11 +328,12 @@ struct BPiece<GGML_IQ3_S> {
       lk.g[k] = grid[qsb | (((qh >> k) & 1) << 8)];
     }
   }
-  template <int SUB>
-  __device__ static void convert(const Head& hd, const Raw& r, const uint32_t*, const Look& lk, uint32_t out[16]) {
+  template <int S2>
+  __device__ __forceinline__ static void convert_hp(const Head& hd, const Raw& r, const uint32_t*, int p,
+                                                    const Look& lk, uint32_t out[16]) {
     const uint32_t s = hd.s;
     const uint32_t h = (threadIdx.x >> 5) & 1;
-    const int ib = 2 * SUB + (int)h;
+    const int ib = 4 * S2 + 2 * p + (int)h;
     // block byte offsets: signs at 74 + 4 ib (= s + 2 mod 4), scales at 106, d at 0
     const uint32_t s2 = (s + 2) & 3;
     const uint32_t sg = alignbyte(r.sg[1], r.sg[0], s2);
@@ -294,9 +346,9 @@ struct BPiece<GGML_IQ3_S> {
     // packed first, then bits 2p and 2p + 1 of sg are moved to bits 15 and 31 by one packed
     // 16-bit shift of sg's half-word (in both halves) and xored in
     const uint32_t sgw[2] = {(sg & 0xFFFFu) | (sg << 16), (sg >> 16) | (sg & 0xFFFF0000u)};
-    auto pair_signs = [&](int p) {
-      const int q = (2 * p) & 15;
-      const u16x2_t v = __builtin_bit_cast(u16x2_t, sgw[p >> 3]) << u16x2_t{(uint16_t)(15 - q), (uint16_t)(14 - q)};
+    auto pair_signs = [&](int pr) {
+      const int q = (2 * pr) & 15;
+      const u16x2_t v = __builtin_bit_cast(u16x2_t, sgw[pr >> 3]) << u16x2_t{(uint16_t)(15 - q), (uint16_t)(14 - q)};
       return __builtin_bit_cast(uint32_t, v) & 0x80008000u;
     };
 #pragma unroll
@@ -308,11 +360,29 @@ struct BPiece<GGML_IQ3_S> {
       out[2 * k + 1] = f2bf2(y[2], y[3]) ^ pair_signs(2 * k + 1);
     }
   }
+  template <int S2>
+  __device__ __forceinline__ static void decode_hp(const Head& hd, const Raw& r, const uint32_t* grid, int p,
+                                                   uint32_t out[16]) {
+    Look lk;
+    lookup_hp<S2>(hd, r, grid, p, lk);
+    convert_hp<S2>(hd, r, grid, p, lk, out);
+  }
+  // the <SUB> forms through the run-time parity bodies
+  template <int SUB>
+  __device__ static void load(const uint8_t* row, int sb, int h, const uint32_t* grid, Raw& r) {
+    load_hp<SUB / 2>(row, sb, h, SUB & 1, grid, r);
+  }
+  template <int SUB>
+  __device__ static void lookup(const Head& hd, const Raw& r, const uint32_t* grid, Look& lk) {
+    lookup_hp<SUB / 2>(hd, r, grid, SUB & 1, lk);
+  }
+  template <int SUB>
+  __device__ static void convert(const Head& hd, const Raw& r, const uint32_t* grid, const Look& lk, uint32_t out[16]) {
+    convert_hp<SUB / 2>(hd, r, grid, SUB & 1, lk, out);
+  }
   template <int SUB>
   __device__ static void decode(const Head& hd, const Raw& r, const uint32_t* grid, uint32_t out[16]) {
-    Look lk;
-    lookup<SUB>(hd, r, grid, lk);
-    convert<SUB>(hd, r, grid, lk, out);
+    decode_hp<SUB / 2>(hd, r, grid, SUB & 1, out);
   }
   __device__ static int off0(int h) { return 32 * h; }
   __device__ static int off1(int h) { return 32 * h + 16; }

@@ -183,8 +183,8 @@ static int scratch_of_current_device(void** out) {
 }
 
 int ktmi_moe_layer_mode(const ktmi_layer* L, int64_t tokens, int64_t top_k) {
-  (void)L;
-  return tokens * top_k <= kGemvMaxRoutes ? KTMI_MODE_GEMV : KTMI_MODE_GROUPED;
+  if (tokens * top_k > kGemvMaxRoutes) return KTMI_MODE_GROUPED;
+  return L && decode_mfma_fits(L, tokens, top_k) ? KTMI_MODE_DECODE : KTMI_MODE_GEMV;
 }
 
 static int64_t gemv_layer_workspace(const ktmi_layer* L, int64_t tokens, int64_t top_k) {
@@ -228,6 +228,7 @@ int64_t ktmi_moe_layer_pass_tokens(const ktmi_layer* L, int64_t top_k) {
 int64_t ktmi_moe_layer_workspace(const ktmi_layer* L, int64_t tokens, int64_t top_k, int mode) {
   if (!L || tokens < 0 || top_k <= 0) return 0;
   if (mode == KTMI_MODE_AUTO) mode = ktmi_moe_layer_mode(L, tokens, top_k);
+  if (mode == KTMI_MODE_DECODE) return decode_mfma_fits(L, tokens, top_k) ? decode_mfma_workspace(L, tokens, top_k) : 0;
   if (mode == KTMI_MODE_GEMV)
     return decode_layer_fits(L, tokens, top_k) ? decode_layer_workspace(L, tokens, top_k)
                                                : gemv_layer_workspace(L, tokens, top_k);
@@ -253,6 +254,13 @@ int ktmi_moe_layer(const ktmi_layer* L, const void* x, const float* topk_w, cons
   hipStream_t s = (hipStream_t)stream;
   const int64_t R = tokens * top_k;
   const int64_t K = L->hidden, N = L->inter;
+  if (mode == KTMI_MODE_DECODE) {
+    KTMI_REQUIRE(decode_mfma_fits(L, tokens, top_k), KTMI_EINVAL,
+                 "moe_layer: the decode mode takes at most %d routes of %d tokens (and down rows of at most %d bytes "
+                 "per 8-row block)", DM_MAX_ROUTES, DM_MAX_TOKENS, DM_DOWN_WAVE_LDS);
+    return launch_decode_mfma(L, (const uint16_t*)x, topk_w, slot_ids, tokens, top_k, (uint16_t*)y, (uint8_t*)workspace,
+                              s);
+  }
   if (mode == KTMI_MODE_GEMV && decode_layer_fits(L, tokens, top_k))
     return launch_decode_layer(L, (const uint16_t*)x, topk_w, slot_ids, tokens, top_k, (uint16_t*)y,
                                (uint8_t*)workspace, s);

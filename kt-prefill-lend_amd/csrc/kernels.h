@@ -36,6 +36,17 @@ int64_t decode_layer_workspace(const ktmi_layer* L, int64_t tokens, int64_t top_
 int launch_decode_layer(const ktmi_layer* L, const uint16_t* x, const float* topk_w, const int32_t* slot_ids,
                         int64_t tokens, int64_t top_k, uint16_t* y, uint8_t* ws, hipStream_t stream);
 
+// Decode-sized layer on the matrix cores (decode_mfma.hip): two launches for up to
+// DM_MAX_ROUTES routes of at most DM_MAX_TOKENS tokens; the down kernel's waves stage the
+// rows of their slots in LDS regions of DM_DOWN_WAVE_LDS bytes.
+constexpr int DM_MAX_ROUTES = 256;
+constexpr int DM_MAX_TOKENS = 64;
+constexpr int DM_DOWN_WAVE_LDS = 16 * 1024;
+bool decode_mfma_fits(const ktmi_layer* L, int64_t tokens, int64_t top_k);
+int64_t decode_mfma_workspace(const ktmi_layer* L, int64_t tokens, int64_t top_k);
+int launch_decode_mfma(const ktmi_layer* L, const uint16_t* x, const float* topk_w, const int32_t* slot_ids,
+                       int64_t tokens, int64_t top_k, uint16_t* y, uint8_t* ws, hipStream_t stream);
+
 // Grouped prefill path (moe_gemm.hip).
 struct GroupedPlan {
   int64_t routes;      // tokens * top_k

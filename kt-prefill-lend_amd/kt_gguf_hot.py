@@ -41,7 +41,7 @@ DispatchOutput = namedtuple("DispatchOutput", ["hidden_states", "topk_output"])
 TopKOutput = namedtuple("TopKOutput", ["topk_weights", "topk_ids", "router_logits"])
 
 GGML_Q8_0 = 8
-_MODES = {"auto": _lib.MODE_AUTO, "gemv": _lib.MODE_GEMV, "grouped": _lib.MODE_GROUPED}
+_MODES = {"auto": _lib.MODE_AUTO, "gemv": _lib.MODE_GEMV, "grouped": _lib.MODE_GROUPED, "decode": _lib.MODE_DECODE}
 
 
 def _log(msg):

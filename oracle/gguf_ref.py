@@ -487,7 +487,8 @@ def ffn_reference(x_bf16_bits: np.ndarray, slot_ids: np.ndarray, w: np.ndarray,
         wg = w13_deq[e, :N].astype(np.float64)
         wu = w13_deq[e, N:].astype(np.float64)
         g = h @ wg.T
-        a = g / (1.0 + np.exp(-g)) * (h @ wu.T)
+        with np.errstate(over="ignore"):  # exp(-g) = inf for g < -709: silu(g) = -0, as it should
+            a = g / (1.0 + np.exp(-g)) * (h @ wu.T)
         o = (a @ w2_deq[e].astype(np.float64).T) * np.asarray(w, np.float64)[rows, cols][:, None]
         np.add.at(ref, rows, o)
     return ref

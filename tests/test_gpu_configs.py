@@ -64,10 +64,11 @@ def test_q8_0_512_tokens(dev):
     _check(dev, "q8_0-h2048-n768-e128-k8-hot16", 512, L.MODE_AUTO, 1)
 
 
-@pytest.mark.parametrize("T", [1, 4, 8, 16])
-def test_q4_k_decode_windows(dev, T):
+@pytest.mark.parametrize("mode", ["decode", "gemv"])
+@pytest.mark.parametrize("T", [1, 4, 8, 16, 32])
+def test_q4_k_decode_windows(dev, T, mode):
     L, _, _ = _pkg()
-    _check(dev, "q4_k-h2048-n512-e256-k8-hot32-decode", T, L.MODE_AUTO, 1)
+    _check(dev, "q4_k-h2048-n512-e256-k8-hot32-decode", T, L.MODE_DECODE if mode == "decode" else L.MODE_GEMV, 1)
 
 
 @pytest.mark.parametrize("T", [2048, 32768])

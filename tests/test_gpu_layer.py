@@ -53,11 +53,11 @@ CASES = [
 
 
 @pytest.mark.parametrize("case", CASES, ids=[c[0].split("-")[0] for c in CASES])
-@pytest.mark.parametrize("mode", ["gemv", "grouped"])
+@pytest.mark.parametrize("mode", ["gemv", "decode", "grouped"])
 def test_layer_vs_ffn_reference(dev, case, mode):
     L, _, _ = _pkg()
     w, xb, tw, slot, w13, w2 = _case(*case)
-    m = L.MODE_GEMV if mode == "gemv" else L.MODE_GROUPED
+    m = {"gemv": L.MODE_GEMV, "decode": L.MODE_DECODE, "grouped": L.MODE_GROUPED}[mode]
     got = R.bf16_to_f32(_run(dev, w, xb, tw, slot, w13, w2, m))
     g, d = dequant_w(w13, w2, w.types, w.hidden, w.inter)
     ref = R.ffn_reference(xb, slot, tw, g, d)
@@ -126,14 +126,45 @@ def test_decode_at_the_fused_route_limit(dev, T):
     assert np.all(got[(slot < 0).all(axis=1)] == 0)
 
 
-@pytest.mark.parametrize("mode", ["gemv", "grouped"])
+@pytest.mark.parametrize("mode", ["gemv", "decode", "grouped"])
 def test_layer_deterministic(dev, mode):
     L, _, _ = _pkg()
-    w, xb, tw, slot, w13, w2 = _case("q4_k+q6_k-h2048-n512-e256-k8-hot40-prefill", 300, 512, 256, 8, 32)
-    m = L.MODE_GEMV if mode == "gemv" else L.MODE_GROUPED
+    T = 24 if mode == "decode" else 300  # the decode mode takes at most 256 routes
+    w, xb, tw, slot, w13, w2 = _case("q4_k+q6_k-h2048-n512-e256-k8-hot40-prefill", T, 512, 256, 8, 32)
+    m = {"gemv": L.MODE_GEMV, "decode": L.MODE_DECODE, "grouped": L.MODE_GROUPED}[mode]
     a = _run(dev, w, xb, tw, slot, w13, w2, m)
     b = _run(dev, w, xb, tw, slot, w13, w2, m)
     assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("t13,t2", [(R.GGML_Q4_K, R.GGML_Q6_K), (R.GGML_Q8_0, R.GGML_Q8_0), (R.GGML_IQ3_S, R.GGML_IQ3_S)])
+def test_decode_mode_column_groups(dev, t13, t2):
+    """The decode mode with slots of 64, 33, 17 and 1 routes (4, 3, 2 and 1 groups of 16 MFMA
+    columns), 64 tokens x top-4 = 256 routes: against the fp64 FFN, and within the layer
+    tolerance of the GEMV mode."""
+    L, H, S = _pkg()
+    base = S.WORKLOADS["q4_k+q6_k-h2048-n512-e256-k8-hot40-prefill"]
+    w = replace(base, hidden=512, inter=256, hot=8, experts=32, top_k=4, types=(t13, t13, t2))
+    T = 64
+    rng = np.random.default_rng(21)
+    slot = np.full((T, 4), -1, np.int32)
+    slot[:, 0] = 0                      # slot 0: every token
+    slot[:33, 1] = 1                    # slot 1: 33 tokens
+    slot[5:22, 2] = 2                   # slot 2: 17 tokens
+    slot[40, 2] = 3                     # slot 3: one token
+    others = rng.integers(4, w.hot, size=(T, 1))
+    slot[:, 3:] = np.where(rng.random((T, 1)) < 0.5, others, -1)
+    tw = rng.random((T, 4)).astype(np.float32)
+    tw /= tw.sum(axis=1, keepdims=True)
+    xb = S.activations(w, T)
+    w13, w2 = S.slot_tensors(w)
+    got = R.bf16_to_f32(_run(dev, w, xb, tw, slot, w13, w2, L.MODE_DECODE))
+    g, d = dequant_w(w13, w2, w.types, w.hidden, w.inter)
+    ref = R.ffn_reference(xb, slot, tw, g, d)
+    l2, l1, cos = R.rel_errors(got, ref)
+    assert l2 < TOL_REL_L2 and cos > 0.999, (l2, l1, cos)
+    gemv = R.bf16_to_f32(_run(dev, w, xb, tw, slot, w13, w2, L.MODE_GEMV))
+    assert R.rel_errors(got, gemv)[0] < TOL_REL_L2
 
 
 def test_grouped_edge_cases(dev):
@@ -209,14 +240,14 @@ def test_grouped_at_full_shape(dev):
     assert l2 < TOL_REL_L2 and cos > 0.999, (l2, l1, cos)
 
 
-@pytest.mark.parametrize("mode", ["gemv", "grouped"])
+@pytest.mark.parametrize("mode", ["gemv", "decode", "grouped"])
 def test_layer_empty_input_and_foreign_ids(dev, mode):
     """T = 0 is a no-op; slot ids >= S or < -1 (experts owned by no slot here) behave exactly
     like -1."""
     import torch
 
     L, H, _ = _pkg()
-    m = L.MODE_GEMV if mode == "gemv" else L.MODE_GROUPED
+    m = {"gemv": L.MODE_GEMV, "decode": L.MODE_DECODE, "grouped": L.MODE_GROUPED}[mode]
     w, xb, tw, slot, w13, w2 = _case("q4_k+q6_k-h2048-n512-e256-k8-hot40-prefill", 24, 512, 256, 8, 32)
     W13, W2 = to_dev(w13, dev), to_dev(w2, dev)
     desc = H.layer_desc(W13, W2, w.hidden, w.inter, w.types[0], w.types[2])
@@ -256,7 +287,7 @@ def test_grouped_headline_chunk_properties(dev):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("mode", ["gemv", "grouped"])
+@pytest.mark.parametrize("mode", ["gemv", "decode", "grouped"])
 def test_layer_in_hip_graph(dev, mode):
     """The layer call captured in a HIP graph (no memsets, no host sync inside): every replay,
     with eager layer calls on other inputs between the replays, reproduces the eager output
@@ -264,8 +295,8 @@ def test_layer_in_hip_graph(dev, mode):
     import torch
 
     L, H, _ = _pkg()
-    m = L.MODE_GEMV if mode == "gemv" else L.MODE_GROUPED
-    w, xb, tw, slot, w13, w2 = _case("q4_k+q6_k-h2048-n512-e256-k8-hot40-prefill", 12 if mode == "gemv" else 300,
+    m = {"gemv": L.MODE_GEMV, "decode": L.MODE_DECODE, "grouped": L.MODE_GROUPED}[mode]
+    w, xb, tw, slot, w13, w2 = _case("q4_k+q6_k-h2048-n512-e256-k8-hot40-prefill", 12 if mode != "grouped" else 300,
                                      512, 256, 8, 32)
     W13, W2 = to_dev(w13, dev), to_dev(w2, dev)
     desc = H.layer_desc(W13, W2, w.hidden, w.inter, w.types[0], w.types[2])
@@ -292,7 +323,8 @@ def test_layer_in_hip_graph(dev, mode):
         torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("mode,T", [("grouped", 48), ("grouped", 4096), ("gemv", 8), ("gemv", 64)])
+@pytest.mark.parametrize("mode,T", [("grouped", 48), ("grouped", 4096), ("gemv", 8), ("gemv", 64), ("decode", 8),
+                                    ("decode", 32)])
 def test_slot_address_table_matches_contiguous_slots(dev, mode, T):
     """Slots given as a device table of per-slot addresses (w_is_table, each slot its own
     allocation, in reverse order) give the same bits as the contiguous slot tensors: 128- and
@@ -305,7 +337,7 @@ def test_slot_address_table_matches_contiguous_slots(dev, mode, T):
     xb = S.activations(w, T)
     w13, w2 = S.slot_tensors(w)
     W13, W2 = to_dev(w13, dev), to_dev(w2, dev)
-    m = L.MODE_GEMV if mode == "gemv" else L.MODE_GROUPED
+    m = {"gemv": L.MODE_GEMV, "decode": L.MODE_DECODE, "grouped": L.MODE_GROUPED}[mode]
     x, twd, sd = bf16_tensor(xb, dev), to_dev(tw, dev), to_dev(slot, dev)
     ref = H.moe_layer(H.layer_desc(W13, W2, w.hidden, w.inter, w.types[0], w.types[2]), x, twd, sd, m)
     n = W13.shape[0]

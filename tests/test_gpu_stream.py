@@ -168,7 +168,7 @@ def test_selftest_logs_agreement(dev, monkeypatch, capsys):
     acc = st.run(method, None, do, ids_d)
     torch.cuda.synchronize()
     log = capsys.readouterr().out
-    m = re.search(r"self-check of layer 0 .*rel L2 (\S+), cos (\S+)", log)
+    m = re.search(r"self-check of layer 0 .*rel L2 ([0-9.eE+-]+), cos ([0-9.eE+-]+)", log)
     assert m, log
     rel, cos = float(m.group(1)), float(m.group(2))
     assert rel < 2e-2 and cos > 0.999, log

@@ -54,8 +54,11 @@ def test_layer_workspace_sizes():
 
     L = _lib.lib()
     d = _lib.ktmi_layer(hidden=2048, inter=512, n_slots=40, type13=12, type2=14)
-    assert L.ktmi_moe_layer_mode(d, 4, 8) == _lib.MODE_GEMV
+    assert L.ktmi_moe_layer_mode(d, 4, 8) == _lib.MODE_DECODE
     assert L.ktmi_moe_layer_mode(d, 16384, 8) == _lib.MODE_GROUPED
+    # the decode mode's workspace: h [R, inter] bf16
+    assert L.ktmi_moe_layer_workspace(d, 4, 8, _lib.MODE_DECODE) == 4 * 8 * 512 * 2
+    assert L.ktmi_moe_layer_workspace(d, 65, 2, _lib.MODE_DECODE) == 0  # past its 64 tokens
     g = L.ktmi_moe_layer_workspace(d, 16384, 8, _lib.MODE_GROUPED)
     R_ = 16384 * 8
     assert g >= R_ * (512 + 2048) * 2 + R_ * 4
@@ -382,6 +385,11 @@ def test_layer_argument_errors_before_device_work():
     assert rc == -1 and b"aligned" in L.ktmi_last_error()
     rc = L.ktmi_moe_layer(d, p, p, p, 10000, 8, p, p, big, _lib.MODE_GEMV, 0)
     assert rc == -1 and b"65535" in L.ktmi_last_error()
+    rc = L.ktmi_moe_layer(d, p, p, p, 40, 8, p, p, big, _lib.MODE_DECODE, 0)  # 320 routes
+    assert rc == -1 and b"decode mode" in L.ktmi_last_error()
+    assert L.ktmi_moe_layer_mode(d, 16, 8) == _lib.MODE_DECODE
+    assert L.ktmi_moe_layer_mode(d, 33, 8) == _lib.MODE_GROUPED
+    assert L.ktmi_moe_layer_mode(d, 128, 2) == _lib.MODE_GEMV  # 128 tokens: past the decode mode's 64
 
 
 @pytest.mark.parametrize("hidden,inter,top_k,pass_tokens", [(7168, 2048, 8, 37376), (2048, 512, 8, 130816),
