@@ -330,12 +330,15 @@ def bench_configs(P, torch, S, ev, dev, steps=10, warmup=2):
 
 
 def bench_decode(P, torch, S, ev, dev, steps=50, warmup=5, rotate_bytes=512e6):
-    """Decode-shaped layer (Q4_K, 32 hot slots) at 1/4/8/16 tokens: GB/s against HBM.
-    "hbm": the weights rotate over enough copies that the copies' touched bytes exceed
-    `rotate_bytes` (twice the 256 MB Infinity Cache) at every T; "warm": one copy. GB/s =
-    algorithmic bytes / step time (both kernels and the gap between them). "floor": the same
-    byte count read by one plain reduction kernel over rotated buffers, and the time of two
-    back-to-back launches of a one-element kernel (the two-launch layer's fixed cost)."""
+    """Decode-shaped layer (Q4_K, 32 hot slots) at 1/4/8/16 tokens: GB/s against HBM, for the
+    decode mode (KTMI_MODE_DECODE, the library's choice from 64 routes) and the GEMV mode (the
+    reference kernels' int8 numerics, its choice below 64 routes). Per mode: "hbm", the weights rotating over enough copies that the
+    copies' touched bytes exceed `rotate_bytes` (twice the 256 MB Infinity Cache) at every T;
+    "warm", one copy; "graph", the same rotated steps captured in one HIP graph and replayed
+    (no host issue cost between the layers). GB/s = algorithmic bytes / step time (every launch
+    of the step and the gaps between them). "floor": graph-replayed references on the same stream, two
+    back-to-back launches of a one-block kernel per step, and a device-to-device copy of the
+    step's touched weight bytes from the rotated copies (it reads them and writes as many)."""
     H, L = P.kt_gguf_hot, P._lib
     w = S.WORKLOADS[DECODE]
     w13, w2 = S.slot_tensors(w)
@@ -359,47 +362,110 @@ def bench_decode(P, torch, S, ev, dev, steps=50, warmup=5, rotate_bytes=512e6):
         tw_d, slot_d = torch.from_numpy(tw).to(dev), torch.from_numpy(slot).to(dev)
         nbytes = uniq * exp_bytes + 2 * T * w.hidden * 2
         out = {}
-        for name, dl in (("hbm", descs[:nc]), ("warm", descs[:1])):
-            ms, stages, _, _ = time_layer(P, torch, dl, x, tw_d, slot_d, L.MODE_GEMV, steps, warmup, ev, sample_every=0)
+        for mname, mode in (("decode", L.MODE_DECODE), ("gemv", L.MODE_GEMV)):
+            rec = {}
+            for name, dl in (("hbm", descs[:nc]), ("warm", descs[:1])):
+                ms, stages, _, _ = time_layer(P, torch, dl, x, tw_d, slot_d, mode, steps, warmup, ev, sample_every=0)
+                gbs = nbytes / (ms * 1e-3) / 1e9
+                rec[name] = {"ms_per_step": round(ms, 4), "GBps": round(gbs, 1),
+                             "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+                             "stage_ms_with_events": {k: round(v, 4) for k, v in stages.items()}}
+            ms = time_layer_graph(P, torch, descs[:nc], x, tw_d, slot_d, mode, steps, ev)
             gbs = nbytes / (ms * 1e-3) / 1e9
-            out[name] = {"ms_per_step": round(ms, 4), "GBps": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
-                         "stage_ms_with_events": {k: round(v, 4) for k, v in stages.items()}}
-        out["hbm"]["copies"], out["hbm"]["rotated_bytes"] = nc, nc * uniq * exp_bytes
-        out["floor"] = decode_floor(torch, ev, dev, uniq * exp_bytes, nc, steps)
+            rec["graph"] = {"ms_per_step": round(ms, 4), "GBps": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+            out[mname] = rec
+        out["copies"], out["rotated_bytes"] = nc, nc * uniq * exp_bytes
+        out["floor"] = decode_floor(P, torch, ev, dev, copies[:nc], slot, uniq, w, steps)
         res[f"T{T}"] = {"hot_routes": int((slot >= 0).sum()), "unique_experts": uniq, "bytes": nbytes, **out}
         log(f"decode T={T}: {res[f'T{T}']}")
     del copies
     return res
 
 
-def decode_floor(torch, ev, dev, nbytes, ncopy, steps):
-    """Speed-of-light references for a decode step reading `nbytes` of weights: one plain
-    reduction (torch.amax over int32) of nbytes from buffers rotated over `ncopy` copies, and
-    two back-to-back launches of a one-element fill."""
-    L = load_pkg()._lib
-    stream = L.stream_ptr(dev)
-    n = max(1, int(nbytes) // 4)
-    bufs = [torch.ones(n, dtype=torch.int32, device=dev) for _ in range(ncopy)]
-    tiny = torch.zeros(1, dtype=torch.float32, device=dev)
-    se = ev.create(4)
-
-    def timed(fn, a, b):
-        for i in range(3):
-            fn(i)
-        torch.cuda.synchronize()
-        ev.record(se[a], stream)
+def time_layer_graph(P, torch, desc_list, x, w, slot, mode, steps, ev):
+    """`steps` layer calls (rotating through desc_list) captured in one HIP graph on a side
+    stream; the mean step time of a replay (events around the replay on that stream), after
+    two replays to warm up."""
+    H, L = P.kt_gguf_hot, P._lib
+    lib = L.lib()
+    T, k = slot.shape
+    out = torch.empty((T, desc_list[0].hidden), dtype=torch.bfloat16, device=x.device)
+    ws = torch.empty((max(lib.ktmi_moe_layer_workspace(d, T, k, mode) for d in desc_list),), dtype=torch.uint8,
+                     device=x.device)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        for d in desc_list[:2]:
+            H.moe_layer(d, x, w, slot, mode, out, ws)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
         for i in range(steps):
-            fn(i)
-        ev.record(se[b], stream)
-        torch.cuda.synchronize()
-        return ev.ms(se[a], se[b]) / steps
-
-    read_ms = timed(lambda i: torch.amax(bufs[i % ncopy]), 0, 1)
-    launch_ms = timed(lambda i: (tiny.fill_(i), tiny.fill_(i + 1)), 2, 3)
+            H.moe_layer(desc_list[i % len(desc_list)], x, w, slot, mode, out, ws)
+    se = ev.create(2)
+    with torch.cuda.stream(s):
+        g.replay()
+        g.replay()
+        ev.record(se[0], s.cuda_stream)
+        g.replay()
+        ev.record(se[1], s.cuda_stream)
+    torch.cuda.synchronize()
+    ms = ev.ms(se[0], se[1]) / steps
     ev.destroy(se)
-    del bufs
-    return {"read_ms": round(read_ms, 4), "read_GBps": round(4 * n / (read_ms * 1e-3) / 1e9, 1),
-            "two_launches_ms": round(launch_ms, 4)}
+    del g
+    return ms
+
+
+def decode_floor(P, torch, ev, dev, copies, slot, uniq, w, steps):
+    """Graph-replayed references for a decode step (`steps` of them captured in one HIP graph,
+    the mean step of a replay): two back-to-back launches of a one-block kernel (the
+    library's remap over 8 ids), and a device-to-device copy of the step's touched weight
+    bytes (the unique hot slots' w13 and w2, from the next of the rotated copies each step:
+    a read of those bytes from HBM and a write of as many)."""
+    L = P._lib
+    lib = L.lib()
+    ids = torch.zeros(8, dtype=torch.int32, device=dev)
+    loc = torch.empty(8, dtype=torch.int32, device=dev)
+    hot = sorted(set(slot[slot >= 0].tolist()))
+    dst13 = torch.empty((len(hot),) + tuple(copies[0][0].shape[1:]), dtype=torch.uint8, device=dev)
+    dst2 = torch.empty((len(hot),) + tuple(copies[0][1].shape[1:]), dtype=torch.uint8, device=dev)
+    idx = torch.tensor(hot, dtype=torch.int64, device=dev)
+    # the touched slots as contiguous sources in every copy (the copy leg reads exactly them)
+    src = [(c13.index_select(0, idx), c2.index_select(0, idx)) for c13, c2 in copies]
+
+    def launches(_i, st):
+        for _ in range(2):
+            L.check(lib.ktmi_remap_ids(ids.data_ptr(), 8, 0, 4, loc.data_ptr(), st), "remap_ids")
+
+    def copy(i, st):
+        a, b = src[i % len(src)]
+        dst13.copy_(a, non_blocking=True)
+        dst2.copy_(b, non_blocking=True)
+
+    out = {}
+    for name, fn in (("two_launches_ms", launches), ("copy_ms", copy)):
+        s = torch.cuda.Stream()
+        with torch.cuda.stream(s):
+            fn(0, s.cuda_stream)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for i in range(steps):
+                fn(i, s.cuda_stream)
+        se = ev.create(2)
+        with torch.cuda.stream(s):
+            g.replay()
+            ev.record(se[0], s.cuda_stream)
+            g.replay()
+            ev.record(se[1], s.cuda_stream)
+        torch.cuda.synchronize()
+        out[name] = round(ev.ms(se[0], se[1]) / steps, 4)
+        ev.destroy(se)
+        del g
+    nb = dst13.numel() + dst2.numel()
+    out["copy_bytes_read"] = nb
+    out["copy_read_GBps"] = round(nb / (out["copy_ms"] * 1e-3) / 1e9, 1)
+    del src
+    return out
 
 
 def bench_hybrid(P, torch, S, ev, dev, distinct=16, reps=200, warmup=10, rotate=8):

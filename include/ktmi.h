@@ -135,8 +135,8 @@ int64_t ktmi_moe_layer_workspace(const ktmi_layer* layer, int64_t tokens, int64_
 int ktmi_moe_layer(const ktmi_layer* layer, const void* x, const float* topk_w, const int32_t* slot_ids,
                    int64_t tokens, int64_t top_k, void* y, void* workspace, int64_t ws_bytes, int mode,
                    void* stream);
-/* The mode KTMI_MODE_AUTO picks for this many routes: GROUPED above 256 routes, else DECODE
- * where it applies, else GEMV. */
+/* The mode KTMI_MODE_AUTO picks for this many routes: GROUPED above 256 routes, DECODE from
+ * 64 routes where it applies, else GEMV. */
 int ktmi_moe_layer_mode(const ktmi_layer* layer, int64_t tokens, int64_t top_k);
 /* Tokens per pass of KTMI_MODE_GROUPED: a longer call runs as consecutive passes over token
  * slices of this size (each token's output depends only on its own routes), and the

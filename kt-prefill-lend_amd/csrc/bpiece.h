@@ -68,8 +68,12 @@ struct GMem {
   __device__ __forceinline__ static T ld(const void* p) { return gload<T>(p); }
 };
 struct LMem {
+  // the LDS offset is the generic address's low 32 bits (an address-space cast of a generic
+  // pointer would add a null check that the compiler here lowers wrongly)
   template <typename T>
-  __device__ __forceinline__ static T ld(const void* p) { return *(const __attribute__((address_space(3))) T*)p; }
+  __device__ __forceinline__ static T ld(const void* p) {
+    return *(const __attribute__((address_space(3))) T*)(uint32_t)(uintptr_t)p;
+  }
 };
 
 template <int TYPE>

@@ -182,9 +182,16 @@ static int scratch_of_current_device(void** out) {
   return KTMI_OK;
 }
 
+// Below 64 routes the GEMV mode's two launches beat the decode mode's three (graph-replayed
+// steps of the 2048 x 512 Q4_K layer with 32 hot slots: 13.8 against 16.1 us at 8 routes,
+// 20.4 against 21.2 at 32); from 64 routes the decode mode's MFMAs win (25.3 against 26.7 at
+// 64, 26.4 against 31.8 at 128).
+constexpr int64_t kDecodeMinRoutes = 64;
+
 int ktmi_moe_layer_mode(const ktmi_layer* L, int64_t tokens, int64_t top_k) {
   if (tokens * top_k > kGemvMaxRoutes) return KTMI_MODE_GROUPED;
-  return L && decode_mfma_fits(L, tokens, top_k) ? KTMI_MODE_DECODE : KTMI_MODE_GEMV;
+  return L && tokens * top_k >= kDecodeMinRoutes && decode_mfma_fits(L, tokens, top_k) ? KTMI_MODE_DECODE
+                                                                                       : KTMI_MODE_GEMV;
 }
 
 static int64_t gemv_layer_workspace(const ktmi_layer* L, int64_t tokens, int64_t top_k) {

@@ -1,4 +1,4 @@
-// Decode-sized hot-expert layer on the matrix cores (KTMI_MODE_DECODE): two launches for up
+// Decode-sized hot-expert layer on the matrix cores (KTMI_MODE_DECODE): three launches for up
 // to DM_MAX_ROUTES routes and DM_MAX_TOKENS tokens, the weights decoded from their GGUF
 // blocks straight into v_mfma_f32_16x16x32_bf16 operands (bpiece.h: the exact dequantised
 // values, one bf16 rounding, the values the grouped prefill kernels and the dequant entry
@@ -9,11 +9,11 @@
 //                   owns and multiplies them against the bf16 x rows of the slot's routes;
 //                   the partial sums meet in LDS, h = bf16(silu(g) * u) (the grouped
 //                   epilogue's) goes to h [R, N] of the routes.
-//   dm_down_combine block (8 hidden rows): each wave stages the rows of its slots (every
-//                   eighth slot with routes) in LDS with direct loads issued at once, runs
-//                   them against the h rows of the slots' routes, rounds each route's output
-//                   to bf16 (the reference's per-route bf16 output) in LDS; then the weighted
-//                   top-k sum in k order (hot/kt_gguf_hot.py:43-71) of the block's rows.
+//   dm_down         block (k-th slot with routes, 64 hidden rows): each wave stages 16 down
+//                   rows of the slot in LDS by direct loads, runs them against the h rows of
+//                   the slot's routes and writes each route's outputs, rounded to bf16 (the
+//                   reference's per-route bf16 output), to yv [R, K].
+//   dm_combine      the weighted top-k sum in k order (hot/kt_gguf_hot.py:43-71).
 //
 // Lane map (16x16x32 operands): row or column l % 16, k-chunk g = l / 16 (8 values). Lane
 // group g holds the piece of BPiece step SUB = 2 s + (g & 1), half g >> 1 of each 128-value
@@ -28,8 +28,8 @@
 // a slot with 12 routes costs what a slot with one does.
 //
 // Membership (the k-th slot with routes, a slot's routes) is computed by every wave on its
-// own from the slot ids (ballots and a 16-word bitmap in LDS private to the wave): no block
-// barrier before the weight loads are issued.
+// own from the slot ids (ballots, and a 16-word slot bitmap ORed over the wave by DPP into
+// scalar registers): no block barrier before the weight loads are issued.
 #include <type_traits>
 
 #include "bpiece.h"
@@ -41,14 +41,14 @@ namespace {
 
 constexpr int DM_WAVES = 4;                   // gate/up block: waves over the hidden dimension
 constexpr int DM_THREADS = DM_WAVES * 64;
-constexpr int DM_RI = 16;                     // intermediate rows per gate/up block
-constexpr int DM_CG = DM_MAX_TOKENS / 16;     // 16-route column groups of a slot, at most
-constexpr int DN_WAVES = 8;                   // down block: waves over the slots
+constexpr int DM_RT = 16;                     // intermediate rows per gate/up block
+constexpr int DN_WAVES = 4;                   // down block: waves over the block's hidden rows
 constexpr int DN_THREADS = DN_WAVES * 64;
-constexpr int DN_RH = 8;                      // hidden rows per down block (MFMA rows 8..15 repeat them)
-constexpr int DN_WREG = DM_DOWN_WAVE_LDS;     // staged down rows per wave and round
+constexpr int DN_ROWS = 16;                   // hidden rows per down wave (the MFMA's rows)
+constexpr int DN_TILE = DN_WAVES * DN_ROWS;   // hidden rows per down block
+constexpr int DN_WREG = DM_DOWN_WAVE_LDS;     // a wave's staged down rows
 static_assert(DM_MAX_ROUTES <= 256, "four routes a lane");
-static_assert(DM_MAX_TOKENS % 16 == 0 && DN_THREADS >= DN_RH * DM_MAX_TOKENS, "combine: a thread per (token, row)");
+static_assert(DM_MAX_TOKENS % 16 == 0, "column groups of 16 routes");
 
 __device__ __forceinline__ f32x4_t mfma16(const bf16x8_t& a, const bf16x8_t& b, const f32x4_t& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -83,42 +83,59 @@ struct WaveRoutes {
   }
 };
 
-// The slots with routes as a bitmap of 16 words (S <= 512) in LDS private to the wave; lane
-// w < 16 keeps word w and the number of slots with routes in words 0..w.
+// OR of a 32-bit value over the wave, in scalar registers: DPP inside each row of 16 lanes
+// (quad swaps, then the half-row and row mirrors), then the four rows' values read out
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_or(uint32_t v) {
+  return v | (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ uint32_t wave_or(uint32_t v) {
+  asm volatile("" : "+v"(v));  // a vector register: the compiler may otherwise feed DPP a scalar one
+  v = dpp_or<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = dpp_or<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = dpp_or<0x141>(v);  // row_half_mirror
+  v = dpp_or<0x140>(v);  // row_mirror
+  return (uint32_t)(__builtin_amdgcn_readlane((int)v, 0) | __builtin_amdgcn_readlane((int)v, 16) |
+                    __builtin_amdgcn_readlane((int)v, 32) | __builtin_amdgcn_readlane((int)v, 48));
+}
+
+// The slots with routes as 16 words of 32 slots (S <= 512), the same in every lane (scalar
+// registers): each word is the OR over the wave of the lanes' own route bits.
 struct SlotSet {
-  uint32_t word;
-  int incl, total;
-  __device__ __forceinline__ void build(const WaveRoutes& wr, uint32_t* bm) {
-    const int lane = threadIdx.x & 63;
-    if (lane < 16) bm[lane] = 0u;
-    wave_fence();  // a wave's LDS operations run in order; the fences keep the compiler's order
+  static constexpr int NW = 16;
+  uint32_t word[NW];
+  int total;
+  __device__ __forceinline__ void build(const WaveRoutes& wr, int S) {
+    const int nw = (S + 31) >> 5;
+    total = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (wr.sid[i] >= 0) atomicOr(&bm[wr.sid[i] >> 5], 1u << (wr.sid[i] & 31));
-    wave_fence();
-    word = lane < 16 ? bm[lane] : 0u;
-    incl = __popc(word);
+    for (int c = 0; c < NW; ++c) {
+      word[c] = 0u;
+      if (c < nw) {  // uniform
+        uint32_t m = 0u;
 #pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
-      const int t = __shfl_up(incl, o, 64);
-      if (lane >= o) incl += t;
+        for (int i = 0; i < 4; ++i)
+          m |= wr.sid[i] >= 0 && (wr.sid[i] >> 5) == c ? 1u << (wr.sid[i] & 31) : 0u;
+        word[c] = wave_or(m);
+        total += __popc(word[c]);
+      }
     }
-    total = __shfl(incl, 15, 64);
   }
   // the k-th slot with routes in ascending order, -1 past the last (uniform over the wave)
   __device__ __forceinline__ int kth(int k) const {
     if (k >= total) return -1;
-    const int lane = threadIdx.x & 63;
-    const int before = incl - __popc(word);
-    const bool here = lane < 16 && before <= k && k < incl;
-    const int w = __ffsll((unsigned long long)__ballot(here)) - 1;
-    int e = 0;
-    if (here) {
-      uint32_t v = word;
-      for (int j = k - before; j > 0; --j) v &= v - 1u;
-      e = 32 * lane + __ffs(v) - 1;
+    int e = -1;
+#pragma unroll
+    for (int c = 0; c < NW; ++c) {
+      const int n = __popc(word[c]);
+      if (e < 0 && k < n) {  // uniform: the word holding it; its k lowest set bits cleared
+        uint32_t v = word[c];
+        for (int j = k; j > 0; --j) v &= v - 1u;
+        e = 32 * c + __ffs(v) - 1;
+      }
+      k -= n;
     }
-    return __shfl(e, w, 64);
+    return e;
   }
 };
 
@@ -149,43 +166,68 @@ __device__ __forceinline__ int kpos(int p, int h, int j) {
   return BP::template ksub_hp<S2>(p) + BP::coff(q);
 }
 
+// One block per (k-th slot with routes, 16 intermediate rows). The block's 16 gate rows and
+// 16 up rows (two contiguous ranges of the slot tensor, 32 row_bytes(K) bytes) are moved into
+// LDS by direct loads all issued at once, so the weights in flight cost no registers and
+// three blocks share a CU; the 4 waves then take a quarter of the hidden dimension each,
+// decode their share of the staged rows into MFMA operands and multiply them with the x rows
+// of the slot's routes (loaded into registers behind the direct loads); the partial sums
+// meet in LDS and h = bf16(silu(g) * u) goes to h [R, N] of the routes.
 template <int TYPE>
 __global__ __launch_bounds__(DM_THREADS) void dm_gate_up(const uint16_t* __restrict__ x, int K, int N,
                                                          const int32_t* __restrict__ slot_ids, int R, int S,
                                                          int top_k, const uint8_t* __restrict__ W13, int w_is_table,
                                                          int64_t w_stride, uint16_t* __restrict__ hbuf) {
   using BP = BPiece<TYPE>;
-  __shared__ float part[DM_WAVES][DM_CG][2][4][64];  // the waves' partial sums, [tile: gate, up]
-  __shared__ int scratch[DM_WAVES][16 + DM_MAX_TOKENS];
-  __shared__ uint32_t grid[TYPE == GGML_IQ3_S ? 512 : 1];
+  // one LDS object (see the down kernel): staged rows, the waves' partial sums, their
+  // scratch, the IQ3_S codebook
+  constexpr int PART_OFF = DM_GU_LDS;
+  constexpr int SCR_OFF = PART_OFF + DM_WAVES * 2 * 4 * 64 * 4;
+  constexpr int GRID_OFF = SCR_OFF + DM_WAVES * (16 + DM_MAX_TOKENS) * 4;
+  constexpr int LDS_BYTES = GRID_OFF + (TYPE == GGML_IQ3_S ? 2048 : 16);
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[LDS_BYTES];
+  float (*part)[2][4][64] = (float(*)[2][4][64])(smem + PART_OFF);  // [wave][tile: gate, up]
+  int (*scratch)[16 + DM_MAX_TOKENS] = (int(*)[16 + DM_MAX_TOKENS])(smem + SCR_OFF);
+  uint32_t* grid = (uint32_t*)(smem + GRID_OFF);
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int G = N / DM_RI;
+  const int G = N / DM_RT;
   const int kslot = blockIdx.x / G, rg = blockIdx.x - kslot * G;
   if constexpr (TYPE == GGML_IQ3_S) stage_iq3s_grid(grid);
   WaveRoutes wr;
   wr.load(slot_ids, R, S);
   SlotSet ss;
-  ss.build(wr, (uint32_t*)scratch[wave]);
+  ss.build(wr, S);
   const int e = ss.kth(kslot);
   if (e < 0) return;  // the same in every wave: past the slots with routes
+  // the slot's routes and the first 16 routes' x rows before any direct load into LDS: the
+  // compiler makes an LDS access after such loads wait for them
   int* mem = scratch[wave] + 16;
   const int m = slot_routes(wr, e, mem);
-  const int ncg = (m + 15) >> 4;  // <= DM_CG: at most DM_MAX_TOKENS tokens
-
+  const int ncg = (m + 15) >> 4;  // 16-route column groups
   const int r = lane & 15, p = (lane >> 4) & 1, h = (lane >> 5) & 1;
+  const uint32_t x_bytes = (uint32_t)(R / top_k) * (uint32_t)K * 2u;
+  uint32_t xoff = r < m ? (uint32_t)(mem[r] / top_k) * (uint32_t)K * 2u : x_bytes;
   const int64_t rb = row_bytes(K, TYPE);
-  const uint8_t* wexp = w_is_table ? (const uint8_t*)((const int64_t*)W13)[e] : W13 + (int64_t)e * w_stride;
-  const uint8_t* wrow[2] = {wexp + (int64_t)(DM_RI * rg + r) * rb, wexp + (int64_t)(N + DM_RI * rg + r) * rb};
+  const int range = DM_RT * (int)rb;  // bytes of 16 rows, a multiple of 16
+  {
+    // the gate range at smem, the up range at smem + range: 1 KB pieces over the waves, the
+    // last piece of a range moved back to end at the range's end (its bytes written twice,
+    // with the same values)
+    const uint8_t* wexp = w_is_table ? (const uint8_t*)((const int64_t*)W13)[e] : W13 + (int64_t)e * w_stride;
+    const int npc = (range + 1023) >> 10;
+    for (int q = wave; q < 2 * npc; q += DM_WAVES) {  // uniform per wave
+      const int t = q >= npc, qi = q - t * npc;
+      const int off = min(qi << 10, range - 1024);  // range >= 1024: decode_mfma_fits
+      const uint8_t* src = wexp + ((int64_t)(t ? N : 0) + (int64_t)DM_RT * rg) * rb;
+      const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, (uint32_t)range, 0x00020000);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (__attribute__((address_space(3))) void*)(smem + t * range + off), 16,
+                                               off + 16 * lane, 0, 0, 0);
+    }
+  }
+  const uint8_t* wrow[2] = {smem + r * (int)rb, smem + range + r * (int)rb};  // staged gate row r, up row r
   // activation operand: column c = 16 cg + r is the slot's c-th route (its token's x row);
   // columns past the routes read past the buffer, which returns zeros
-  const uint32_t x_bytes = (uint32_t)(R / top_k) * (uint32_t)K * 2u;
   const __amdgpu_buffer_rsrc_t x_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, x_bytes, 0x00020000);
-  uint32_t xoff[DM_CG];
-#pragma unroll
-  for (int cg = 0; cg < DM_CG; ++cg) {
-    const int c = 16 * cg + r;
-    xoff[cg] = c < m ? (uint32_t)(mem[c] / top_k) * (uint32_t)K * 2u : x_bytes;
-  }
   int kp[2][4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -196,156 +238,135 @@ __global__ __launch_bounds__(DM_THREADS) void dm_gate_up(const uint16_t* __restr
     const u32x4_t v = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, off + 2u * (uint32_t)(256 * sb + k), 0, 0));
     return __builtin_bit_cast(bf16x8_t, v);
   };
-
   // this wave's super-block columns
   const int nsb = K / 256;
   const int per = (nsb + DM_WAVES - 1) / DM_WAVES;
   const int sb0 = wave * per, sb1 = min(nsb, sb0 + per);
-
-  struct Stage {
-    typename BP::Head hd[2];
-    typename BP::Raw raw[2][2];
-    bf16x8_t xb[2][4];
-  };
-  auto issue = [&](int sb, Stage& st) {
+  f32x4_t acc[2][2];  // [tile: gate, up][two in turn, so back-to-back MFMAs do not wait for each other]
+  // a super-block column of both tiles against the activation operands xb[S2][j]
+  auto compute = [&](int sb, const bf16x8_t (&xb)[2][4]) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      BP::load_head(wrow[t], sb, h, st.hd[t]);
-      BP::template load_hp<0>(wrow[t], sb, h, p, grid, st.raw[t][0]);
-      BP::template load_hp<1>(wrow[t], sb, h, p, grid, st.raw[t][1]);
-    }
+      typename BP::Head hd;
+      typename BP::Raw raw[2];
+      BP::template load_head<LMem>(wrow[t], sb, h, hd);
+      BP::template load_hp<0, LMem>(wrow[t], sb, h, p, grid, raw[0]);
+      BP::template load_hp<1, LMem>(wrow[t], sb, h, p, grid, raw[1]);
+      uint32_t a[16];
+      BP::template decode_hp<0>(hd, raw[0], grid, p, a);
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+      for (int j = 0; j < 4; ++j) acc[t][j & 1] = mfma16(words8(&a[4 * j]), xb[0][j], acc[t][j & 1]);
+      BP::template decode_hp<1>(hd, raw[1], grid, p, a);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) st.xb[s][j] = xload(xoff[0], sb, kp[s][j]);
-  };
-
-  f32x4_t acc[DM_CG][2];
-#pragma unroll
-  for (int cg = 0; cg < DM_CG; ++cg) acc[cg][0] = acc[cg][1] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-
-  auto compute = [&](int sb, const Stage& st, auto s2c) {
-    constexpr int S2 = decltype(s2c)::value;
-    uint32_t a[2][16];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) BP::template decode_hp<S2>(st.hd[t], st.raw[t][S2], grid, p, a[t]);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      acc[0][0] = mfma16(words8(&a[0][4 * j]), st.xb[S2][j], acc[0][0]);
-      acc[0][1] = mfma16(words8(&a[1][4 * j]), st.xb[S2][j], acc[0][1]);
-    }
-#pragma unroll
-    for (int cg = 1; cg < DM_CG; ++cg) {
-      if (cg < ncg) {  // uniform: slots with more than 16 routes
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const bf16x8_t xb = xload(xoff[cg], sb, kp[S2][j]);
-          acc[cg][0] = mfma16(words8(&a[0][4 * j]), xb, acc[cg][0]);
-          acc[cg][1] = mfma16(words8(&a[1][4 * j]), xb, acc[cg][1]);
-        }
-      }
+      for (int j = 0; j < 4; ++j) acc[t][j & 1] = mfma16(words8(&a[4 * j]), xb[1][j], acc[t][j & 1]);
     }
   };
-
-  using Z0 = std::integral_constant<int, 0>;
-  using Z1 = std::integral_constant<int, 1>;
-  // two stages in turn, the next super-block's loads issued before this one's MFMAs (with
-  // K = 2048 a wave's two super-blocks are all in flight before the first MFMA)
-  Stage sa, sbuf;
-  if (sb0 < sb1) issue(sb0, sa);
-  if constexpr (TYPE == GGML_IQ3_S) __syncthreads();  // the codebook
-  for (int sb = sb0; sb < sb1; sb += 2) {
-    if (sb + 1 < sb1) issue(sb + 1, sbuf);
-    compute(sb, sa, Z0{});
-    compute(sb, sa, Z1{});
-    if (sb + 1 < sb1) {
-      if (sb + 2 < sb1) issue(sb + 2, sa);
-      compute(sb + 1, sbuf, Z0{});
-      compute(sb + 1, sbuf, Z1{});
-    }
-  }
-
-#pragma unroll
-  for (int cg = 0; cg < DM_CG; ++cg)
-    if (cg < ncg)
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) part[wave][cg][t][i][lane] = acc[cg][t][i];
-  __syncthreads();
   // output (row rr, column c): lane 16 (rr / 4) + c of each wave holds it as element rr % 4;
   // 16 consecutive threads write one route's 16 values of h (32 bytes)
   const int c = threadIdx.x >> 4, rr = threadIdx.x & 15;
   const int ln = 16 * (rr >> 2) + c, i = rr & 3;
+  // one pass per 16 routes of the slot (a second one only past 16 routes)
   for (int cg = 0; cg < ncg; ++cg) {
+    if (cg > 0) xoff = 16 * cg + r < m ? (uint32_t)(mem[16 * cg + r] / top_k) * (uint32_t)K * 2u : x_bytes;
+    acc[0][0] = acc[0][1] = acc[1][0] = acc[1][1] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    // the x operands of two super-block columns in flight (all of a wave's with K = 2048)
+    bf16x8_t xa[2][4], xc[2][4];
+    auto xissue = [&](int sb, bf16x8_t (&xb)[2][4]) {
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xb[s2][j] = xload(xoff, sb, kp[s2][j]);
+    };
+    if (sb0 < sb1) xissue(sb0, xa);
+    if (sb0 + 1 < sb1) xissue(sb0 + 1, xc);
+    if (cg == 0) {
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the staged rows (and the x operands)
+      __syncthreads();                    // every wave's pieces; the IQ3_S codebook
+    }
+    for (int sb = sb0; sb < sb1; sb += 2) {
+      compute(sb, xa);
+      if (sb + 2 < sb1) xissue(sb + 2, xa);
+      if (sb + 1 < sb1) {
+        compute(sb + 1, xc);
+        if (sb + 3 < sb1) xissue(sb + 3, xc);
+      }
+    }
+    if (cg > 0) __syncthreads();  // the previous pass has read the partial sums
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) part[wave][t][q][lane] = acc[t][0][q] + acc[t][1][q];
+    __syncthreads();
     const int col = 16 * cg + c;
     if (col < m) {
       float g = 0.0f, u = 0.0f;
 #pragma unroll
       for (int w = 0; w < DM_WAVES; ++w) {
-        g += part[w][cg][0][i][ln];
-        u += part[w][cg][1][i][ln];
+        g += part[w][0][i][ln];
+        u += part[w][1][i][ln];
       }
-      hbuf[(int64_t)mem[col] * N + DM_RI * rg + rr] = f2bf(dm_silu_mul(g, u));
+      hbuf[(int64_t)mem[col] * N + DM_RT * rg + rr] = f2bf(dm_silu_mul(g, u));
     }
   }
 }
 
-// One block per DN_RH hidden rows; NSB = N / 256 when it is small (0: any N, a loop). Wave w takes the slots with routes w, w + DN_WAVES, ...:
-// per round, as many as its LDS region holds, their DN_RH rows (contiguous in the slot
-// tensor) moved into LDS by direct loads all issued at once; then slot by slot, the h rows
-// of the slot's routes (the next slot's issued before this one's MFMAs) against the decoded
-// rows. Each route's output is rounded to bf16 into LDS; the block ends with the weighted
-// top-k sum in k order.
-template <int TYPE, int NSB>
-__global__ __launch_bounds__(DN_THREADS) void dm_down_combine(const uint16_t* __restrict__ hbuf, int K, int N,
-                                                              const int32_t* __restrict__ slot_ids,
-                                                              const float* __restrict__ topk_w, int T, int top_k,
-                                                              int S, const uint8_t* __restrict__ W2, int w_is_table,
-                                                              int64_t w_stride, uint16_t* __restrict__ y) {
+// One block per (k-th slot with routes, DN_TILE hidden rows); wave w takes the tile's rows
+// 16 w .. 16 w + 15. A wave moves its 16 down rows of the slot (contiguous in the slot
+// tensor) into its LDS region by direct loads, brings the h rows of the slot's routes into
+// registers behind them (L2 hits: every block of the slot reads the same rows), decodes the
+// rows into MFMA operands and writes each route's 16 outputs, rounded to bf16 (the
+// reference's per-route bf16 output), to yv [R, K]. The weighted top-k sum is a launch of its
+// own (dm_combine): inside this one, the blocks of a tile would have to order themselves
+// through device-scope fences, which write back and invalidate the whole L2 of their XCD.
+template <int TYPE>
+__global__ __launch_bounds__(DN_THREADS) void dm_down(const uint16_t* __restrict__ hbuf, int K, int N,
+                                                      const int32_t* __restrict__ slot_ids, int R, int S,
+                                                      const uint8_t* __restrict__ W2, int w_is_table, int64_t w_stride,
+                                                      uint16_t* __restrict__ yv) {
   using BP = BPiece<TYPE>;
-  // one LDS object (with several, the compiler makes every LDS read wait for all direct
-  // loads into LDS, including the h loads meant to stay in flight): per wave its staged
-  // rows, then the routes' outputs, the waves' scratch, hot flags and route weights, the
-  // IQ3_S codebook
-  constexpr int YV_OFF = DN_WAVES * DN_WREG;
-  constexpr int SCR_INTS = 16 + DM_MAX_TOKENS + 2 * (DN_WREG / 1024);  // bitmap, routes, row addresses
-  constexpr int SCR_OFF = YV_OFF + DM_MAX_ROUTES * DN_RH * 4;
-  constexpr int HOT_OFF = SCR_OFF + DN_WAVES * SCR_INTS * 4;
-  constexpr int WTS_OFF = HOT_OFF + DM_MAX_ROUTES * 4;
-  constexpr int GRID_OFF = WTS_OFF + DM_MAX_ROUTES * 4;
+  // one LDS object: per wave its staged rows, then the waves' route lists, the IQ3_S codebook
+  constexpr int MEM_OFF = DN_WAVES * DN_WREG;
+  constexpr int GRID_OFF = MEM_OFF + DN_WAVES * DM_MAX_TOKENS * 4;
   constexpr int LDS_BYTES = GRID_OFF + (TYPE == GGML_IQ3_S ? 2048 : 16);
-  static_assert(LDS_BYTES <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[LDS_BYTES];
-  float (*yv)[DN_RH] = (float(*)[DN_RH])(smem + YV_OFF);
-  int (*scratch)[SCR_INTS] = (int(*)[SCR_INTS])(smem + SCR_OFF);
-  int* hot = (int*)(smem + HOT_OFF);
-  float* wts = (float*)(smem + WTS_OFF);
   uint32_t* grid = (uint32_t*)(smem + GRID_OFF);
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int R = T * top_k;
-  const int c0 = blockIdx.x * DN_RH;
+  const int ntile = K / DN_TILE;
+  const int kslot = blockIdx.x / ntile, tile = blockIdx.x - kslot * ntile;
+  const int c0 = tile * DN_TILE;
   if constexpr (TYPE == GGML_IQ3_S) stage_iq3s_grid(grid);
-  if (threadIdx.x < R) {
-    const int s = slot_ids[threadIdx.x];
-    hot[threadIdx.x] = s >= 0 && s < S;
-    wts[threadIdx.x] = topk_w[threadIdx.x];
-  }
   WaveRoutes wr;
   wr.load(slot_ids, R, S);
   SlotSet ss;
-  ss.build(wr, (uint32_t*)scratch[wave]);
-  int* mem = scratch[wave] + 16;
-  if constexpr (TYPE == GGML_IQ3_S) __syncthreads();  // the codebook
-
-  // MFMA row r holds block row r % DN_RH: rows 8..15 repeat 0..7 and their outputs are unused
+  ss.build(wr, S);
+  const int e = ss.kth(kslot);
+  if (e < 0) return;  // the same in every wave: past the slots with routes
+  // the slot's routes and the first column group's h offsets before any direct load into
+  // LDS: the compiler makes an LDS access after such loads wait for them
+  int* mem = (int*)(smem + MEM_OFF) + DM_MAX_TOKENS * wave;
+  const int m = slot_routes(wr, e, mem);
+  const int ncg = (m + 15) >> 4;
   const int r = lane & 15, p = (lane >> 4) & 1, h = (lane >> 5) & 1;
+  const uint32_t hrow = 2u * (uint32_t)N;
+  const uint32_t h_bytes = (uint32_t)R * hrow;
+  // column c = 16 cg + r of the operand is the slot's c-th route; past the routes the
+  // offset lies past the buffer, whose loads return zeros
+  uint32_t hoff = r < m ? (uint32_t)mem[r] * hrow : h_bytes;
   const int64_t rb = row_bytes(N, TYPE);
-  const int slot_bytes = DN_RH * (int)rb;
-  const int slot_lds = (slot_bytes + 1023) & ~1023;  // whole 64-lane direct loads
-  const int per_round = DN_WREG / slot_lds;          // >= 1: decode_mfma_fits
-  const int nsb = N / 256;
-  const uint32_t h_bytes = (uint32_t)R * (uint32_t)N * 2u;
+  const int wbytes = DN_ROWS * (int)rb;  // a multiple of 16, at most DN_WREG (decode_mfma_fits)
+  const int rw0 = c0 + DN_ROWS * wave;
+  uint8_t* const region = smem + wave * DN_WREG;
+  {
+    const uint8_t* wexp = w_is_table ? (const uint8_t*)((const int64_t*)W2)[e] : W2 + (int64_t)e * w_stride;
+    const __amdgpu_buffer_rsrc_t w_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(wexp + (int64_t)rw0 * rb), (short)0, (uint32_t)wbytes, 0x00020000);
+    // 1 KB a wave instruction; the lanes past the end of the last piece stay idle
+    for (int q0 = 0; q0 < wbytes; q0 += 1024)
+      if (q0 + 16 * lane < wbytes)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (__attribute__((address_space(3))) void*)(region + q0), 16,
+                                                 q0 + 16 * lane, 0, 0, 0);
+  }
+  const uint8_t* wrow = region + r * (int)rb;
   const __amdgpu_buffer_rsrc_t h_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)hbuf, (short)0, h_bytes, 0x00020000);
   int kp[2][4];
 #pragma unroll
@@ -357,97 +378,97 @@ __global__ __launch_bounds__(DN_THREADS) void dm_down_combine(const uint16_t* __
     const u32x4_t v = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(h_rsrc, off + 2u * (uint32_t)(256 * sb + k), 0, 0));
     return __builtin_bit_cast(bf16x8_t, v);
   };
-
-  uint64_t* waddr = (uint64_t*)(scratch[wave] + 16 + DM_MAX_TOKENS);  // the round's row addresses
-  for (int k0 = wave; k0 < ss.total; k0 += DN_WAVES * per_round) {
-    // this round: the wave's slots k0, k0 + DN_WAVES, ... (per_round of them at most). Their
-    // rows' addresses first (a slot table read is waited for before any direct load is
-    // issued, so that no wait for it drains them), then every direct load at once.
-    int nk = 0;
-    for (int k = k0; k < ss.total && nk < per_round; k += DN_WAVES, ++nk) {
-      const int e = ss.kth(k);
-      const uint8_t* wexp = w_is_table ? (const uint8_t*)((const int64_t*)W2)[e] : W2 + (int64_t)e * w_stride;
-      if (lane == 0) waddr[nk] = (uint64_t)(uintptr_t)(wexp + (int64_t)c0 * rb);
-    }
-    wave_fence();
-    for (int n = 0; n < nk; ++n) {
-      const uint64_t a = waddr[n];  // the same in every lane: scalar registers for the resource
-      const uint64_t au = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a) |
-                          ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32)) << 32);
-      const __amdgpu_buffer_rsrc_t w_rsrc =
-          __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)au, (short)0, (uint32_t)slot_bytes, 0x00020000);
-      uint8_t* dst = smem + wave * DN_WREG + n * slot_lds;
-      for (int q0 = 0; q0 < slot_bytes; q0 += 1024)  // pieces past the rows read zeros (within slot_lds)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (__attribute__((address_space(3))) void*)(dst + q0), 16,
-                                                 q0 + 16 * lane, 0, 0, 0);
-    }
-    // the slots in turn; h of the next slot's routes is loaded before this one's MFMAs
-    struct HOps { bf16x8_t v[2][4]; };
-    auto hissue = [&](uint32_t off, int sb, HOps& o) {
+  const int nsb = N / 256;
+  f32x4_t acc[2];
+  // one super-block column against the operands hb[S2][j]; two accumulators in turn, so
+  // back-to-back MFMAs do not wait for each other
+  auto compute = [&](int sb, const bf16x8_t (&hb)[2][4]) {
+    typename BP::Head hd;
+    typename BP::Raw raw[2];
+    BP::template load_head<LMem>(wrow, sb, h, hd);
+    BP::template load_hp<0, LMem>(wrow, sb, h, p, grid, raw[0]);
+    BP::template load_hp<1, LMem>(wrow, sb, h, p, grid, raw[1]);
+    uint32_t a[16];
+    BP::template decode_hp<0>(hd, raw[0], grid, p, a);
 #pragma unroll
-      for (int s = 0; s < 2; ++s)
+    for (int j = 0; j < 4; ++j) acc[j & 1] = mfma16(words8(&a[4 * j]), hb[0][j], acc[j & 1]);
+    BP::template decode_hp<1>(hd, raw[1], grid, p, a);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) o.v[s][j] = hload(off, sb, kp[s][j]);
+    for (int j = 0; j < 4; ++j) acc[j & 1] = mfma16(words8(&a[4 * j]), hb[1][j], acc[j & 1]);
+  };
+  for (int cg = 0; cg < ncg; ++cg) {
+    if (cg > 0) hoff = 16 * cg + r < m ? (uint32_t)mem[16 * cg + r] * hrow : h_bytes;
+    acc[0] = acc[1] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    bf16x8_t ha[2][4], hc[2][4];  // two super-block columns in flight
+    auto hissue = [&](int sb, bf16x8_t (&hb)[2][4]) {
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) hb[s2][j] = hload(hoff, sb, kp[s2][j]);
     };
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's staged rows (the only loads so far)
-    wave_fence();
-    for (int n = 0; n < nk; ++n) {
-      const int e = ss.kth(k0 + n * DN_WAVES);
-      const int m = slot_routes(wr, e, mem);
-      const uint8_t* wrow = smem + wave * DN_WREG + n * slot_lds + (r % DN_RH) * (int)rb;
-      for (int cg = 0; cg * 16 < m; ++cg) {
-        const int col = 16 * cg + r;
-        const uint32_t hoff = col < m ? (uint32_t)mem[col] * (uint32_t)N * 2u : h_bytes;
-        f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        auto step = [&](int sb, const HOps& ho) {
-          typename BP::Head hd;
-          typename BP::Raw raw[2];
-          uint32_t a[2][16];
-          BP::template load_head<LMem>(wrow, sb, h, hd);
-          BP::template load_hp<0, LMem>(wrow, sb, h, p, grid, raw[0]);
-          BP::template load_hp<1, LMem>(wrow, sb, h, p, grid, raw[1]);
-          BP::template decode_hp<0>(hd, raw[0], grid, p, a[0]);
-          BP::template decode_hp<1>(hd, raw[1], grid, p, a[1]);
-#pragma unroll
-          for (int s = 0; s < 2; ++s)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc = mfma16(words8(&a[s][4 * j]), ho.v[s][j], acc);
-        };
-        if constexpr (NSB > 0) {
-          // every h operand of the slot's columns issued at once, then the super-blocks in
-          // turn (straight-line code: the compiler counts each wait)
-          HOps ho[NSB];
-#pragma unroll
-          for (int sb = 0; sb < NSB; ++sb) hissue(hoff, sb, ho[sb]);
-#pragma unroll
-          for (int sb = 0; sb < NSB; ++sb) step(sb, ho[sb]);
-        } else {
-          for (int sb = 0; sb < nsb; ++sb) {
-            HOps ho;
-            hissue(hoff, sb, ho);
-            step(sb, ho);
-          }
-        }
-        // output rows 4 (lane / 16) + i (< DN_RH: lanes 0..31), column lane % 16
-        if (lane < 2 * 16 && col < m) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) yv[mem[col]][4 * (lane >> 4) + i] = bf2f(f2bf(acc[i]));
-        }
+    hissue(0, ha);
+    if (nsb > 1) hissue(1, hc);
+    if (cg == 0) {
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the staged rows (and the h operands)
+      wave_fence();
+      if constexpr (TYPE == GGML_IQ3_S) __syncthreads();  // the codebook
+    }
+    for (int sb = 0; sb < nsb; sb += 2) {
+      compute(sb, ha);
+      if (sb + 2 < nsb) hissue(sb + 2, ha);
+      if (sb + 1 < nsb) {
+        compute(sb + 1, hc);
+        if (sb + 3 < nsb) hissue(sb + 3, hc);
       }
-      wave_fence();  // mem is rewritten for the next slot
+    }
+    // lane l holds rows 4 (l / 16) + i of column l % 16: four consecutive bf16 of yv
+    const int col = 16 * cg + r;
+    if (col < m) {
+      const int rt = mem[col];
+      const uint32_t lo = (uint32_t)f2bf(acc[0][0] + acc[1][0]) | ((uint32_t)f2bf(acc[0][1] + acc[1][1]) << 16);
+      const uint32_t hi = (uint32_t)f2bf(acc[0][2] + acc[1][2]) | ((uint32_t)f2bf(acc[0][3] + acc[1][3]) << 16);
+      *(uint2*)(yv + (int64_t)rt * K + rw0 + 4 * (lane >> 4)) = make_uint2(lo, hi);
     }
   }
-  __syncthreads();
-  // y[t, c0 + i] = bf16( sum over k ascending, hot routes only, of bf16(Y * bf16(w)) )
-  for (int q = threadIdx.x; q < T * DN_RH; q += DN_THREADS) {
-    const int t = q / DN_RH, i = q - t * DN_RH;
-    float accy = 0.0f;
-    for (int k = 0; k < top_k; ++k) {
-      const int rt = t * top_k + k;
-      if (hot[rt]) accy += bf2f(f2bf(yv[rt][i] * bf2f(f2bf(wts[rt]))));
+}
+
+// y[t, c] = bf16( sum over k ascending, hot routes only, of bf16(Y * bf16(w)) ): a thread per
+// (token, eight hidden columns); the loads of eight routes are issued before their sums
+__global__ __launch_bounds__(256) void dm_combine(const uint16_t* __restrict__ yv, const int32_t* __restrict__ slot_ids,
+                                                  const float* __restrict__ topk_w, int T, int top_k, int S, int K,
+                                                  uint16_t* __restrict__ y) {
+  const int q = blockIdx.x * 256 + threadIdx.x;
+  const int G = K / 8;
+  if (q >= T * G) return;
+  const int t = q / G, c = 8 * (q - t * G);
+  float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  for (int k0 = 0; k0 < top_k; k0 += 8) {
+    int sl[8];
+    float w[8];
+    uint4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int rt = t * top_k + min(k0 + u, top_k - 1);  // past top_k: a repeat, not summed
+      sl[u] = slot_ids[rt];
+      w[u] = topk_w[rt];
+      v[u] = *(const uint4*)(yv + (int64_t)rt * K + c);  // every route's row lies in yv
     }
-    y[(int64_t)t * K + c0 + i] = f2bf(accy);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (k0 + u >= top_k || sl[u] < 0 || sl[u] >= S) continue;  // cold or past top_k: its yv row is stale
+      const float wb = bf2f(f2bf(w[u]));
+      const uint32_t wd[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] += bf2f(f2bf(bf2f((uint16_t)(wd[i] & 0xFFFFu)) * wb));
+        acc[2 * i + 1] += bf2f(f2bf(bf2f((uint16_t)(wd[i] >> 16)) * wb));
+      }
+    }
   }
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = (uint32_t)f2bf(acc[2 * i]) | ((uint32_t)f2bf(acc[2 * i + 1]) << 16);
+  *(uint4*)(y + (int64_t)t * K + c) = make_uint4(o[0], o[1], o[2], o[3]);
 }
 
 template <int TYPE>
@@ -457,7 +478,7 @@ int launch_dm_gate_up(const ktmi_layer* L, const uint16_t* x, const int32_t* slo
   const int64_t st13 = 2 * N * row_bytes(K, TYPE);
   // blocks numbered (k-th slot with routes, row group), row group fastest; the blocks past
   // the slots with routes exit at once
-  const unsigned nb = (unsigned)(S < R ? S : R) * (unsigned)(N / DM_RI);
+  const unsigned nb = (unsigned)(S < R ? S : R) * (unsigned)(N / DM_RT);
   dm_gate_up<TYPE><<<nb, DM_THREADS, 0, stream>>>(x, (int)K, (int)N, slot_ids, (int)R, (int)S, (int)top_k,
                                                   (const uint8_t*)L->w13, L->w_is_table, st13, hbuf);
   KTMI_HIP_TRY(hipGetLastError());
@@ -466,20 +487,17 @@ int launch_dm_gate_up(const ktmi_layer* L, const uint16_t* x, const int32_t* slo
 
 template <int TYPE>
 int launch_dm_down(const ktmi_layer* L, const uint16_t* hbuf, const int32_t* slot_ids, const float* topk_w,
-                   int64_t tokens, int64_t top_k, uint16_t* y, hipStream_t stream) {
-  const int64_t K = L->hidden, N = L->inter, S = L->n_slots;
+                   int64_t tokens, int64_t top_k, uint16_t* yv, uint16_t* y, hipStream_t stream) {
+  const int64_t K = L->hidden, N = L->inter, S = L->n_slots, R = tokens * top_k;
   const int64_t st2 = K * row_bytes(N, TYPE);
-#define KTMI_DM_DOWN(NSB)                                                                                      \
-  dm_down_combine<TYPE, NSB><<<(unsigned)(K / DN_RH), DN_THREADS, 0, stream>>>(                                   \
-      hbuf, (int)K, (int)N, slot_ids, topk_w, (int)tokens, (int)top_k, (int)S, (const uint8_t*)L->w2, L->w_is_table, \
-      st2, y)
-  switch (N / 256) {
-    case 1: KTMI_DM_DOWN(1); break;
-    case 2: KTMI_DM_DOWN(2); break;
-    case 3: KTMI_DM_DOWN(3); break;
-    default: KTMI_DM_DOWN(0); break;
-  }
-#undef KTMI_DM_DOWN
+  // blocks numbered (k-th slot with routes, hidden tile), tile fastest; the blocks past the
+  // slots with routes exit at once
+  const unsigned nb = (unsigned)(S < R ? S : R) * (unsigned)(K / DN_TILE);
+  dm_down<TYPE><<<nb, DN_THREADS, 0, stream>>>(hbuf, (int)K, (int)N, slot_ids, (int)R, (int)S, (const uint8_t*)L->w2,
+                                               L->w_is_table, st2, yv);
+  KTMI_HIP_TRY(hipGetLastError());
+  const unsigned nc = (unsigned)((tokens * (K / 8) + 255) / 256);
+  dm_combine<<<nc, 256, 0, stream>>>(yv, slot_ids, topk_w, (int)tokens, (int)top_k, (int)S, (int)K, y);
   KTMI_HIP_TRY(hipGetLastError());
   return KTMI_OK;
 }
@@ -487,20 +505,28 @@ int launch_dm_down(const ktmi_layer* L, const uint16_t* hbuf, const int32_t* slo
 }  // namespace
 
 bool decode_mfma_fits(const ktmi_layer* L, int64_t tokens, int64_t top_k) {
-  const int64_t rb2 = row_bytes(L->inter, L->type2);
-  const int64_t slot_lds = (DN_RH * rb2 + 1023) & ~(int64_t)1023;
-  return tokens * top_k <= DM_MAX_ROUTES && tokens <= DM_MAX_TOKENS && L->n_slots <= 512 && L->hidden % 256 == 0 &&
-         L->inter % 256 == 0 && L->hidden % DN_RH == 0 && slot_lds <= DN_WREG &&
-         (L->type2 != GGML_Q8_0 || L->inter % 256 == 0);
+  if (L->hidden % 256 || L->inter % 256) return false;
+  const int64_t range13 = DM_RT * row_bytes(L->hidden, L->type13);  // 16 gate (or up) rows
+  const int64_t rows2 = DN_ROWS * row_bytes(L->inter, L->type2);    // a down wave's 16 rows
+  return tokens * top_k <= DM_MAX_ROUTES && tokens <= DM_MAX_TOKENS && L->n_slots <= 512 &&
+         L->hidden % DN_TILE == 0 && range13 >= 1024 && 2 * range13 <= DM_GU_LDS && rows2 <= DN_WREG;
 }
 
+namespace {
+int64_t up256(int64_t v) { return (v + 255) & ~(int64_t)255; }
+}  // namespace
+
+// h [R, N] bf16, then yv [R, K] bf16 (the routes' down outputs)
 int64_t decode_mfma_workspace(const ktmi_layer* L, int64_t tokens, int64_t top_k) {
-  return ((tokens * top_k * L->inter * 2) + 255) & ~(int64_t)255;  // h [R, N] bf16
+  const int64_t R = tokens * top_k;
+  return up256(R * L->inter * 2) + up256(R * L->hidden * 2);
 }
 
 int launch_decode_mfma(const ktmi_layer* L, const uint16_t* x, const float* topk_w, const int32_t* slot_ids,
                        int64_t tokens, int64_t top_k, uint16_t* y, uint8_t* ws, hipStream_t stream) {
+  const int64_t R = tokens * top_k;
   uint16_t* hbuf = (uint16_t*)ws;
+  uint16_t* yv = (uint16_t*)(ws + up256(R * L->inter * 2));
   record_stage(0, stream);
   record_stage(1, stream);
   int rc;
@@ -515,10 +541,10 @@ int launch_decode_mfma(const ktmi_layer* L, const uint16_t* x, const float* topk
   record_stage(2, stream);
   record_stage(3, stream);
   switch (L->type2) {
-    case GGML_Q8_0: rc = launch_dm_down<GGML_Q8_0>(L, hbuf, slot_ids, topk_w, tokens, top_k, y, stream); break;
-    case GGML_Q4_K: rc = launch_dm_down<GGML_Q4_K>(L, hbuf, slot_ids, topk_w, tokens, top_k, y, stream); break;
-    case GGML_Q6_K: rc = launch_dm_down<GGML_Q6_K>(L, hbuf, slot_ids, topk_w, tokens, top_k, y, stream); break;
-    case GGML_IQ3_S: rc = launch_dm_down<GGML_IQ3_S>(L, hbuf, slot_ids, topk_w, tokens, top_k, y, stream); break;
+    case GGML_Q8_0: rc = launch_dm_down<GGML_Q8_0>(L, hbuf, slot_ids, topk_w, tokens, top_k, yv, y, stream); break;
+    case GGML_Q4_K: rc = launch_dm_down<GGML_Q4_K>(L, hbuf, slot_ids, topk_w, tokens, top_k, yv, y, stream); break;
+    case GGML_Q6_K: rc = launch_dm_down<GGML_Q6_K>(L, hbuf, slot_ids, topk_w, tokens, top_k, yv, y, stream); break;
+    case GGML_IQ3_S: rc = launch_dm_down<GGML_IQ3_S>(L, hbuf, slot_ids, topk_w, tokens, top_k, yv, y, stream); break;
     default: set_error("decode layer: ggml type %d has no kernel", L->type2); return KTMI_ETYPE;
   }
   record_stage(4, stream);

@@ -37,11 +37,12 @@ int launch_decode_layer(const ktmi_layer* L, const uint16_t* x, const float* top
                         int64_t tokens, int64_t top_k, uint16_t* y, uint8_t* ws, hipStream_t stream);
 
 // Decode-sized layer on the matrix cores (decode_mfma.hip): two launches for up to
-// DM_MAX_ROUTES routes of at most DM_MAX_TOKENS tokens; the down kernel's waves stage the
-// rows of their slots in LDS regions of DM_DOWN_WAVE_LDS bytes.
+// DM_MAX_ROUTES routes of at most DM_MAX_TOKENS tokens; a down wave stages 16 rows of a slot
+// in an LDS region of DM_DOWN_WAVE_LDS bytes.
 constexpr int DM_MAX_ROUTES = 256;
 constexpr int DM_MAX_TOKENS = 64;
-constexpr int DM_DOWN_WAVE_LDS = 16 * 1024;
+constexpr int DM_DOWN_WAVE_LDS = 10 * 1024;
+constexpr int DM_GU_LDS = 40 * 1024;  // gate/up: the block's 16 gate and 16 up rows
 bool decode_mfma_fits(const ktmi_layer* L, int64_t tokens, int64_t top_k);
 int64_t decode_mfma_workspace(const ktmi_layer* L, int64_t tokens, int64_t top_k);
 int launch_decode_mfma(const ktmi_layer* L, const uint16_t* x, const float* topk_w, const int32_t* slot_ids,

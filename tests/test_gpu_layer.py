@@ -55,7 +55,9 @@ CASES = [
 @pytest.mark.parametrize("case", CASES, ids=[c[0].split("-")[0] for c in CASES])
 @pytest.mark.parametrize("mode", ["gemv", "decode", "grouped"])
 def test_layer_vs_ffn_reference(dev, case, mode):
-    L, _, _ = _pkg()
+    L, _, S = _pkg()
+    if mode == "decode":  # at most 256 routes
+        case = (case[0], min(case[1], 256 // S.WORKLOADS[case[0]].top_k)) + tuple(case[2:])
     w, xb, tw, slot, w13, w2 = _case(*case)
     m = {"gemv": L.MODE_GEMV, "decode": L.MODE_DECODE, "grouped": L.MODE_GROUPED}[mode]
     got = R.bf16_to_f32(_run(dev, w, xb, tw, slot, w13, w2, m))

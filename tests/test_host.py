@@ -54,10 +54,11 @@ def test_layer_workspace_sizes():
 
     L = _lib.lib()
     d = _lib.ktmi_layer(hidden=2048, inter=512, n_slots=40, type13=12, type2=14)
-    assert L.ktmi_moe_layer_mode(d, 4, 8) == _lib.MODE_DECODE
+    assert L.ktmi_moe_layer_mode(d, 4, 8) == _lib.MODE_GEMV  # 32 routes: below the decode mode's 64
+    assert L.ktmi_moe_layer_mode(d, 8, 8) == _lib.MODE_DECODE
     assert L.ktmi_moe_layer_mode(d, 16384, 8) == _lib.MODE_GROUPED
-    # the decode mode's workspace: h [R, inter] bf16
-    assert L.ktmi_moe_layer_workspace(d, 4, 8, _lib.MODE_DECODE) == 4 * 8 * 512 * 2
+    # the decode mode's workspace: h [R, inter] bf16 and the routes' outputs [R, hidden] bf16
+    assert L.ktmi_moe_layer_workspace(d, 4, 8, _lib.MODE_DECODE) == 4 * 8 * 512 * 2 + 4 * 8 * 2048 * 2
     assert L.ktmi_moe_layer_workspace(d, 65, 2, _lib.MODE_DECODE) == 0  # past its 64 tokens
     g = L.ktmi_moe_layer_workspace(d, 16384, 8, _lib.MODE_GROUPED)
     R_ = 16384 * 8
