@@ -566,9 +566,10 @@ def bench_hybrid(P, torch, S, ev, dev, distinct=16, reps=200, warmup=10, rotate=
 def bench_stream(P, torch, S, ev, dev, distinct=4, reps=3):
     """Large-expert layers streamed from pinned host memory (hidden 7168, intermediate 2048,
     24 hot Q4_K/Q6_K experts per layer, 6144-token chunk, 4 layers): each layer's experts
-    are one group; layer l+1's copy overlaps layer l's grouped layer. Weights: `distinct`
-    quantised experts repeated over the 24 slots (the bytes moved and the work are those of
-    24 experts). Reports the H2D copy time per layer, the compute time per layer on resident
+    are one group; layer l+1's copy overlaps layer l's grouped layer. Weights: 24 distinct
+    experts, made from `distinct` quantised ones (quantising 24 at this size takes minutes)
+    by rotating their rows, a different rotation per slot, so that no two slots hold the
+    same matrices. Reports the H2D copy time per layer, the compute time per layer on resident
     weights, the pipelined time of the 4 layers, and the overlap efficiency
     (serial - pipelined) / (serial - ideal), ideal = max(copies, computes) + min(copy, compute)."""
     import kt_prefill_lend_amd.kt_stream_prefill as SP
@@ -579,8 +580,10 @@ def bench_stream(P, torch, S, ev, dev, distinct=4, reps=3):
     nl = w.layers
     t0 = time.time()
     parts = [S.expert_weights(w, e, 0, 16) for e in range(distinct)]
-    w13 = np.stack([parts[e % distinct][0] for e in range(w.hot)])
-    w2 = np.stack([parts[e % distinct][1] for e in range(w.hot)])
+    # slot e: base e % distinct with its gate/up and down rows rotated by 97 (e // distinct)
+    w13 = np.stack([np.roll(parts[e % distinct][0], 97 * (e // distinct), axis=0) for e in range(w.hot)])
+    w2 = np.stack([np.roll(parts[e % distinct][1], 97 * (e // distinct), axis=0) for e in range(w.hot)])
+    assert len({w13[e, :8].tobytes() for e in range(w.hot)}) == w.hot  # 24 distinct experts
     banks = [SP.Bank.from_slot_rows(torch.from_numpy(w13), torch.from_numpy(w2), w.inter, w.types) for _ in range(nl)]
     ids, tw, slot, _ = S.routing(w, T)
     x = torch.from_numpy(S.activations(w, T).view(np.int16)).to(dev).view(torch.bfloat16)
