@@ -228,7 +228,8 @@ def main():
         except Exception:  # noqa: BLE001
             return None
 
-    traffic = profiled("traffic.json", "bytes")
+    traffic = profiled("traffic.json", "bytes")  # the median of the profiled runs
+    traffic_range = profiled("traffic.json", "bytes_range")
     mfma_busy = profiled("mfma.json", "mfma_busy")
     clock = profiled("mfma.json", "clock_GHz")
 
@@ -250,6 +251,7 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+                     "traffic_range": traffic_range,
                      "mfma_busy_counter": mfma_busy, "clock_GHz_counter": clock,
                      "layer_frac": round(layer_tflops / PEAK_BF16_TFLOPS, 4),
                      "kernel_ms_timed": {"gate_up": round(timed["gate_up"], 4), "down": round(timed["down"], 4),
