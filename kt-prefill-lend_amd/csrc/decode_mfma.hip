@@ -139,10 +139,10 @@ struct SlotSet {
   }
 };
 
-// The routes of slot e in ascending order at mem[0 .. m) (LDS private to the wave); returns m.
-// A slot holds one expert, which a token routes to at most once, so m <= tokens <=
-// DM_MAX_TOKENS; routes past that (ids repeating a slot within a token) are not computed.
-__device__ __forceinline__ int slot_routes(const WaveRoutes& wr, int e, int* mem) {
+// The routes of slot e in ascending order at mem[0 .. m) (LDS private to the wave, a byte a
+// route: route ids are below DM_MAX_ROUTES = 256); returns m. m <= tokens unless a token
+// lists a slot twice; either way every route of the slot is listed.
+__device__ __forceinline__ int slot_routes(const WaveRoutes& wr, int e, uint8_t* mem) {
   const int lane = threadIdx.x & 63;
   const uint64_t below = (1ull << lane) - 1ull;
   int base = 0;
@@ -151,11 +151,11 @@ __device__ __forceinline__ int slot_routes(const WaveRoutes& wr, int e, int* mem
     const bool hit = wr.sid[i] == e;
     const uint64_t b = __ballot(hit);
     const int at = base + __popcll(b & below);
-    if (hit && at < DM_MAX_TOKENS) mem[at] = 64 * i + lane;
+    if (hit) mem[at] = (uint8_t)(64 * i + lane);
     base += __popcll(b);
   }
   wave_fence();
-  return base < DM_MAX_TOKENS ? base : DM_MAX_TOKENS;
+  return base;
 }
 
 // K offset inside a super-block column of the 8 values lane group (p, h) holds for MFMA j of
@@ -183,11 +183,11 @@ __global__ __launch_bounds__(DM_THREADS) void dm_gate_up(const uint16_t* __restr
   // scratch, the IQ3_S codebook
   constexpr int PART_OFF = DM_GU_LDS;
   constexpr int SCR_OFF = PART_OFF + DM_WAVES * 2 * 4 * 64 * 4;
-  constexpr int GRID_OFF = SCR_OFF + DM_WAVES * (16 + DM_MAX_TOKENS) * 4;
+  constexpr int GRID_OFF = SCR_OFF + DM_WAVES * DM_MAX_ROUTES;
   constexpr int LDS_BYTES = GRID_OFF + (TYPE == GGML_IQ3_S ? 2048 : 16);
   __shared__ __attribute__((aligned(1024))) uint8_t smem[LDS_BYTES];
   float (*part)[2][4][64] = (float(*)[2][4][64])(smem + PART_OFF);  // [wave][tile: gate, up]
-  int (*scratch)[16 + DM_MAX_TOKENS] = (int(*)[16 + DM_MAX_TOKENS])(smem + SCR_OFF);
+  uint8_t (*scratch)[DM_MAX_ROUTES] = (uint8_t(*)[DM_MAX_ROUTES])(smem + SCR_OFF);
   uint32_t* grid = (uint32_t*)(smem + GRID_OFF);
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int G = N / DM_RT;
@@ -201,7 +201,7 @@ __global__ __launch_bounds__(DM_THREADS) void dm_gate_up(const uint16_t* __restr
   if (e < 0) return;  // the same in every wave: past the slots with routes
   // the slot's routes and the first 16 routes' x rows before any direct load into LDS: the
   // compiler makes an LDS access after such loads wait for them
-  int* mem = scratch[wave] + 16;
+  uint8_t* mem = scratch[wave];
   const int m = slot_routes(wr, e, mem);
   const int ncg = (m + 15) >> 4;  // 16-route column groups
   const int r = lane & 15, p = (lane >> 4) & 1, h = (lane >> 5) & 1;
@@ -326,7 +326,7 @@ __global__ __launch_bounds__(DN_THREADS) void dm_down(const uint16_t* __restrict
   using BP = BPiece<TYPE>;
   // one LDS object: per wave its staged rows, then the waves' route lists, the IQ3_S codebook
   constexpr int MEM_OFF = DN_WAVES * DN_WREG;
-  constexpr int GRID_OFF = MEM_OFF + DN_WAVES * DM_MAX_TOKENS * 4;
+  constexpr int GRID_OFF = MEM_OFF + DN_WAVES * DM_MAX_ROUTES;
   constexpr int LDS_BYTES = GRID_OFF + (TYPE == GGML_IQ3_S ? 2048 : 16);
   __shared__ __attribute__((aligned(1024))) uint8_t smem[LDS_BYTES];
   uint32_t* grid = (uint32_t*)(smem + GRID_OFF);
@@ -343,7 +343,7 @@ __global__ __launch_bounds__(DN_THREADS) void dm_down(const uint16_t* __restrict
   if (e < 0) return;  // the same in every wave: past the slots with routes
   // the slot's routes and the first column group's h offsets before any direct load into
   // LDS: the compiler makes an LDS access after such loads wait for them
-  int* mem = (int*)(smem + MEM_OFF) + DM_MAX_TOKENS * wave;
+  uint8_t* mem = smem + MEM_OFF + DM_MAX_ROUTES * wave;
   const int m = slot_routes(wr, e, mem);
   const int ncg = (m + 15) >> 4;
   const int r = lane & 15, p = (lane >> 4) & 1, h = (lane >> 5) & 1;

@@ -169,6 +169,35 @@ def test_decode_mode_column_groups(dev, t13, t2):
     assert R.rel_errors(got, gemv)[0] < TOL_REL_L2
 
 
+def test_decode_mode_repeated_slot(dev):
+    """A slot listed two or three times by a token (168 routes of 64 tokens on slot 0, 11
+    groups of 16 MFMA columns, past the 64 a slot can hold without repeats): every route is
+    computed, against the fp64 FFN (which sums the repeats) and the GEMV mode."""
+    L, H, S = _pkg()
+    base = S.WORKLOADS["q4_k+q6_k-h2048-n512-e256-k8-hot40-prefill"]
+    w = replace(base, hidden=512, inter=256, hot=8, experts=32, top_k=4)
+    T = 64
+    rng = np.random.default_rng(22)
+    slot = np.full((T, 4), -1, np.int32)
+    slot[:, 0] = 0
+    slot[:, 1] = 0
+    slot[:40, 2] = 0
+    slot[40:, 2] = rng.integers(1, w.hot, size=T - 40)
+    slot[:, 3] = np.where(rng.random(T) < 0.5, rng.integers(1, w.hot, size=T), -1)
+    assert (slot == 0).sum() == 168
+    tw = rng.random((T, 4)).astype(np.float32)
+    tw /= tw.sum(axis=1, keepdims=True)
+    xb = S.activations(w, T)
+    w13, w2 = S.slot_tensors(w)
+    got = R.bf16_to_f32(_run(dev, w, xb, tw, slot, w13, w2, L.MODE_DECODE))
+    g, d = dequant_w(w13, w2, w.types, w.hidden, w.inter)
+    ref = R.ffn_reference(xb, slot, tw, g, d)
+    l2, l1, cos = R.rel_errors(got, ref)
+    assert l2 < TOL_REL_L2 and cos > 0.999, (l2, l1, cos)
+    gemv = R.bf16_to_f32(_run(dev, w, xb, tw, slot, w13, w2, L.MODE_GEMV))
+    assert R.rel_errors(got, gemv)[0] < TOL_REL_L2
+
+
 def test_grouped_edge_cases(dev):
     """Empty slots, a single token, all-cold tokens, slots with one route."""
     L, _, _ = _pkg()
