@@ -47,8 +47,7 @@ constexpr int DN_THREADS = DN_WAVES * 64;
 constexpr int DN_ROWS = 16;                   // hidden rows per down wave (the MFMA's rows)
 constexpr int DN_TILE = DN_WAVES * DN_ROWS;   // hidden rows per down block
 constexpr int DN_WREG = DM_DOWN_WAVE_LDS;     // a wave's staged down rows
-static_assert(DM_MAX_ROUTES <= 256, "four routes a lane");
-static_assert(DM_MAX_TOKENS % 16 == 0, "column groups of 16 routes");
+static_assert(DM_MAX_ROUTES <= 256, "four routes a lane; a route id fits a byte");
 
 __device__ __forceinline__ f32x4_t mfma16(const bf16x8_t& a, const bf16x8_t& b, const f32x4_t& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
