@@ -198,8 +198,7 @@ __global__ __launch_bounds__(DM_THREADS) void dm_gate_up(const uint16_t* __restr
   ss.build(wr, S);
   const int e = ss.kth(kslot);
   if (e < 0) return;  // the same in every wave: past the slots with routes
-  // the slot's routes and the first 16 routes' x rows before any direct load into LDS: the
-  // compiler makes an LDS access after such loads wait for them
+  // the slot's routes and the first 16 routes' x offsets before the direct loads into LDS
   uint8_t* mem = scratch[wave];
   const int m = slot_routes(wr, e, mem);
   const int ncg = (m + 15) >> 4;  // 16-route column groups
