@@ -241,22 +241,37 @@ __global__ __launch_bounds__(DM_THREADS) void dm_gate_up(const uint16_t* __restr
   const int per = (nsb + DM_WAVES - 1) / DM_WAVES;
   const int sb0 = wave * per, sb1 = min(nsb, sb0 + per);
   f32x4_t acc[2][2];  // [tile: gate, up][two in turn, so back-to-back MFMAs do not wait for each other]
-  // a super-block column of both tiles against the activation operands xb[S2][j]
-  auto compute = [&](int sb, const bf16x8_t (&xb)[2][4]) {
+  // two super-block columns (sb, and sb + 1 when has1) of both tiles: every LDS read of the
+  // four pieces first, then their decodes and MFMAs (one wave a SIMD at small T: the reads'
+  // latency is paid once, not four times)
+  bf16x8_t xa[2][4], xc[2][4];  // the x operands of the two columns
+  auto compute2 = [&](int sb, bool has1) {
+    typename BP::Head hd[2][2];
+    typename BP::Raw raw[2][2][2];
+    const int sbb = has1 ? sb + 1 : sb;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      typename BP::Head hd;
-      typename BP::Raw raw[2];
-      BP::template load_head<LMem>(wrow[t], sb, h, hd);
-      BP::template load_hp<0, LMem>(wrow[t], sb, h, p, grid, raw[0]);
-      BP::template load_hp<1, LMem>(wrow[t], sb, h, p, grid, raw[1]);
-      uint32_t a[16];
-      BP::template decode_hp<0>(hd, raw[0], grid, p, a);
+    for (int c2 = 0; c2 < 2; ++c2)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[t][j & 1] = mfma16(words8(&a[4 * j]), xb[0][j], acc[t][j & 1]);
-      BP::template decode_hp<1>(hd, raw[1], grid, p, a);
+      for (int t = 0; t < 2; ++t) {
+        const int sc = c2 ? sbb : sb;
+        BP::template load_head<LMem>(wrow[t], sc, h, hd[c2][t]);
+        BP::template load_hp<0, LMem>(wrow[t], sc, h, p, grid, raw[c2][t][0]);
+        BP::template load_hp<1, LMem>(wrow[t], sc, h, p, grid, raw[c2][t][1]);
+      }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[t][j & 1] = mfma16(words8(&a[4 * j]), xb[1][j], acc[t][j & 1]);
+    for (int c2 = 0; c2 < 2; ++c2) {
+      if (c2 == 1 && !has1) break;  // uniform
+      const bf16x8_t (&xb)[2][4] = c2 ? xc : xa;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        uint32_t a[16];
+        BP::template decode_hp<0>(hd[c2][t], raw[c2][t][0], grid, p, a);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[t][j & 1] = mfma16(words8(&a[4 * j]), xb[0][j], acc[t][j & 1]);
+        BP::template decode_hp<1>(hd[c2][t], raw[c2][t][1], grid, p, a);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[t][j & 1] = mfma16(words8(&a[4 * j]), xb[1][j], acc[t][j & 1]);
+      }
     }
   };
   // output (row rr, column c): lane 16 (rr / 4) + c of each wave holds it as element rr % 4;
@@ -268,7 +283,6 @@ __global__ __launch_bounds__(DM_THREADS) void dm_gate_up(const uint16_t* __restr
     if (cg > 0) xoff = 16 * cg + r < m ? (uint32_t)(mem[16 * cg + r] / top_k) * (uint32_t)K * 2u : x_bytes;
     acc[0][0] = acc[0][1] = acc[1][0] = acc[1][1] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     // the x operands of two super-block columns in flight (all of a wave's with K = 2048)
-    bf16x8_t xa[2][4], xc[2][4];
     auto xissue = [&](int sb, bf16x8_t (&xb)[2][4]) {
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2)
@@ -282,12 +296,9 @@ __global__ __launch_bounds__(DM_THREADS) void dm_gate_up(const uint16_t* __restr
       __syncthreads();                    // every wave's pieces; the IQ3_S codebook
     }
     for (int sb = sb0; sb < sb1; sb += 2) {
-      compute(sb, xa);
+      compute2(sb, sb + 1 < sb1);
       if (sb + 2 < sb1) xissue(sb + 2, xa);
-      if (sb + 1 < sb1) {
-        compute(sb + 1, xc);
-        if (sb + 3 < sb1) xissue(sb + 3, xc);
-      }
+      if (sb + 3 < sb1) xissue(sb + 3, xc);
     }
     if (cg > 0) __syncthreads();  // the previous pass has read the partial sums
 #pragma unroll
