@@ -182,10 +182,10 @@ static int scratch_of_current_device(void** out) {
   return KTMI_OK;
 }
 
-// Below 64 routes the GEMV mode's two launches beat the decode mode's three (graph-replayed
-// steps of the 2048 x 512 Q4_K layer with 32 hot slots: 13.8 against 16.1 us at 8 routes,
-// 20.4 against 21.2 at 32); from 64 routes the decode mode's MFMAs win (25.3 against 26.7 at
-// 64, 26.4 against 31.8 at 128).
+// Below 64 routes the GEMV mode's two launches match or beat the decode mode's three
+// (graph-replayed steps of the 2048 x 512 Q4_K layer with 32 hot slots: 13.0 against 15.0 us at
+// 8 routes, 19.5 against 19.2 at 32); from 64 routes the decode mode's MFMAs win (23.0 against
+// 25.8 at 64, 24.2 against 30.9 at 128).
 constexpr int64_t kDecodeMinRoutes = 64;
 
 int ktmi_moe_layer_mode(const ktmi_layer* L, int64_t tokens, int64_t top_k) {
