@@ -4,10 +4,11 @@
 // values, one bf16 rounding, the values the grouped prefill kernels and the dequant entry
 // point use), the routes of one slot as the MFMA's 16 columns.
 //
-//   dm_gate_up      block (k-th slot with routes, 16 intermediate rows): the 4 waves split
-//                   the hidden dimension; each lane decodes the gate row and the up row it
-//                   owns and multiplies them against the bf16 x rows of the slot's routes;
-//                   the partial sums meet in LDS, h = bf16(silu(g) * u) (the grouped
+//   dm_gate_up      block (k-th slot with routes, 16 intermediate rows): the block's 16 gate
+//                   and 16 up rows staged in LDS by direct loads; the 4 waves split the
+//                   hidden dimension, each lane decodes its share of the gate row and the up
+//                   row it owns and multiplies them against the bf16 x rows of the slot's
+//                   routes; the partial sums meet in LDS, h = bf16(silu(g) * u) (the grouped
 //                   epilogue's) goes to h [R, N] of the routes.
 //   dm_down         block (k-th slot with routes, 64 hidden rows): each wave stages 16 down
 //                   rows of the slot in LDS by direct loads, runs them against the h rows of
