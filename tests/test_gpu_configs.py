@@ -1,5 +1,5 @@
 """Each workload of the layer at its real shape on the GPU (grouped MFMA mode for the
-prefill chunks, fused GEMV mode for decode windows): a token sample against the oracle's
+prefill chunks, the GEMV and the MFMA decode modes for decode windows): a token sample against the oracle's
 fp64 FFN over the exactly dequantised weights (relative L2 < 2e-2, cosine > 0.999), plus
 tokens with no hot route exactly zero."""
 import numpy as np
@@ -69,6 +69,15 @@ def test_q8_0_512_tokens(dev):
 def test_q4_k_decode_windows(dev, T, mode):
     L, _, _ = _pkg()
     _check(dev, "q4_k-h2048-n512-e256-k8-hot32-decode", T, L.MODE_DECODE if mode == "decode" else L.MODE_GEMV, 1)
+
+
+@pytest.mark.parametrize("T", [8, 16, 25])
+def test_iq3_s_decode_mode_windows(dev, T):
+    """The decode mode on the IQ3_S workload at its real shape (hidden 2048, top-10: 80 / 160 /
+    250 routes), where its staged rows fit; the Q8_0 and Q6_K rows of hidden 2048 do not
+    (decode_mfma_fits) and those layers take the GEMV mode."""
+    L, _, _ = _pkg()
+    _check(dev, "iq3_s-h2048-n512-e512-k10-hot48", T, L.MODE_DECODE, 1)
 
 
 @pytest.mark.parametrize("T", [2048, 32768])
