@@ -198,6 +198,37 @@ def test_decode_mode_repeated_slot(dev):
     assert R.rel_errors(got, gemv)[0] < TOL_REL_L2
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_decode_mode_random_windows(dev, seed):
+    """The decode mode on random windows: 1 to 64 tokens, top-1 to top-8 (at most 256 routes),
+    slot ids mixing hot slots, -1 and ids past the table, some tokens naming a slot twice;
+    against the fp64 FFN."""
+    L, H, S = _pkg()
+    rng = np.random.default_rng(100 + seed)
+    top_k = int(rng.integers(1, 9))
+    T = int(rng.integers(1, min(64, 256 // top_k) + 1))
+    base = S.WORKLOADS["q4_k+q6_k-h2048-n512-e256-k8-hot40-prefill"]
+    w = replace(base, hidden=512, inter=256, hot=8, experts=32, top_k=top_k)
+    slot = rng.integers(-2, w.hot + 3, size=(T, top_k)).astype(np.int32)
+    slot[slot == -2] = -1
+    if T > 2:
+        slot[1, :] = slot[1, 0]  # one token naming one slot top_k times
+    tw = rng.random((T, top_k)).astype(np.float32)
+    tw /= tw.sum(axis=1, keepdims=True)
+    xb = S.activations(w, T)
+    w13, w2 = S.slot_tensors(w)
+    got = R.bf16_to_f32(_run(dev, w, xb, tw, slot, w13, w2, L.MODE_DECODE))
+    g, d = dequant_w(w13, w2, w.types, w.hidden, w.inter)
+    hot = np.where((slot >= 0) & (slot < w.hot), slot, -1)
+    ref = R.ffn_reference(xb, hot, tw, g, d)
+    print(f"seed {seed}: T {T} top-{top_k}")
+    cold = (hot < 0).all(axis=1)
+    assert np.all(got[cold] == 0)
+    if (~cold).any():
+        l2, l1, cos = R.rel_errors(got[~cold], ref[~cold])
+        assert l2 < TOL_REL_L2 and cos > 0.999, (l2, l1, cos)
+
+
 def test_grouped_edge_cases(dev):
     """Empty slots, a single token, all-cold tokens, slots with one route."""
     L, _, _ = _pkg()
