@@ -263,8 +263,10 @@ int ktmi_moe_layer(const ktmi_layer* L, const void* x, const float* topk_w, cons
   const int64_t K = L->hidden, N = L->inter;
   if (mode == KTMI_MODE_DECODE) {
     KTMI_REQUIRE(decode_mfma_fits(L, tokens, top_k), KTMI_EINVAL,
-                 "moe_layer: the decode mode takes at most %d routes of %d tokens (and down rows of at most %d bytes "
-                 "per 8-row block)", DM_MAX_ROUTES, DM_MAX_TOKENS, DM_DOWN_WAVE_LDS);
+                 "moe_layer: the decode mode takes at most %d routes of %d tokens, at most 512 slots, hidden and "
+                 "intermediate sizes that are multiples of 256, and rows that fit its staging (16 gate and 16 up "
+                 "rows in %d bytes, 16 down rows in %d bytes)",
+                 DM_MAX_ROUTES, DM_MAX_TOKENS, DM_GU_LDS, DM_DOWN_WAVE_LDS);
     return launch_decode_mfma(L, (const uint16_t*)x, topk_w, slot_ids, tokens, top_k, (uint16_t*)y, (uint8_t*)workspace,
                               s);
   }
