@@ -61,6 +61,14 @@ __device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
   return r;
 }
 
+// (a & m) | b as one v_and_or_b32 (opaque to the compiler, which would otherwise split the
+// mask per 16-bit half of a result used as two halves)
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t b) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(b));
+  return r;
+}
+
 // Where a piece's bytes are read from: global memory (through the caches) or LDS (rows a
 // kernel has staged there, at the same offsets as in the row).
 struct GMem {
@@ -279,10 +287,11 @@ struct BPiece<GGML_Q6_K> : NoLookup<BPiece<GGML_Q6_K>> {
 
 template <>
 struct BPiece<GGML_IQ3_S> {
+  // `grid` is the codebook as byte selectors, staged in LDS by stage_iq3s_sel (formats.h).
   // VMEM instructions per load<SUB>: qs (dwordx2 + dword, merged into one dwordx3), the
   // signs (dwordx2) and the qh dword
   static constexpr int NLOAD = 3;
-  static constexpr int VPM = 7;    // VALU instructions the GEMM schedule places after each MFMA
+  static constexpr int VPM = 4;    // VALU instructions the GEMM schedule places after each MFMA
   // d and the 4 scale bytes of the block (dwords below them, realigned at decode)
   struct Head { uint32_t dw, sc0, sc1; uint32_t s; };
   // qs[8] of group ib (3 dwords from below), qh byte's dword, signs[4] (2 dwords from below)
@@ -325,11 +334,21 @@ struct BPiece<GGML_IQ3_S> {
     // block byte offsets: qs at 2 + 8 ib (= s + 2 mod 4), qh at 66 + ib
     const uint32_t s2 = (s + 2) & 3;
     const uint32_t qs0 = alignbyte(r.qs[1], r.qs[0], s2), qs1 = alignbyte(r.qs[2], r.qs[1], s2);
-    const uint32_t qh = (r.qh >> (8 * ((s + 2 + ib) & 3))) & 0xFF;
+    const uint32_t qh = __builtin_amdgcn_ubfe(r.qh, 8 * ((s + 2 + ib) & 3), 8);
+    const uint32_t qh2 = qh | (qh << 16);
+    // the 9-bit indices of groups 2j and 2j + 1 as the two 16-bit halves of one word: their
+    // qs bytes moved to bits 0 and 16 by one v_perm, qh bits 2j and 2j + 1 to bits 8 and 24
+    // by one packed 16-bit shift of qh2 and merged with one v_and_or; each half then becomes
+    // an LDS address with one v_lshlrev_b32_sdwa (2.5 VALU an index instead of 4)
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t qsb = ((k < 4 ? qs0 : qs1) >> (8 * (k & 3))) & 0xFF;
-      lk.g[k] = grid[qsb | (((qh >> k) & 1) << 8)];
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t qsw = j < 2 ? qs0 : qs1;
+      const uint32_t b0 = (2 * j) & 3, b1 = (2 * j + 1) & 3;
+      const uint32_t lo = __builtin_amdgcn_perm(0u, qsw, b0 | 0x0C00u | (b1 << 16) | 0x0C000000u);
+      const u16x2_t hv = __builtin_bit_cast(u16x2_t, qh2) << u16x2_t{(uint16_t)(8 - 2 * j), (uint16_t)(7 - 2 * j)};
+      const uint32_t w = and_or(__builtin_bit_cast(uint32_t, hv), 0x01000100u, lo);
+      lk.g[2 * j] = grid[w & 0xFFFF];
+      lk.g[2 * j + 1] = grid[w >> 16];
     }
   }
   template <int S2>
@@ -345,10 +364,23 @@ struct BPiece<GGML_IQ3_S> {
     const uint32_t nib = (scw >> (8 * (ib >> 1) + 4 * (ib & 1))) & 15;
     const uint32_t dbits = (hd.dw >> (8 * s)) & 0xFFFF;
     const float db = half_bits_to_float(dbits) * (float)(1 + 2 * (int)nib);
-    // value 4k + j takes sign bit 4k + j of sg. (sign ? -v : v) of v = db * grid byte flips
-    // the sign bit of v, and so of its bf16 rounding: the pair of values 2p, 2p + 1 is
-    // packed first, then bits 2p and 2p + 1 of sg are moved to bits 15 and 31 by one packed
-    // 16-bit shift of sg's half-word (in both halves) and xored in
+    // A group has only eight magnitudes m = 2e + 1: bf16(db * m) of each (the same rounding
+    // of the same exact product as a value-by-value decode) goes into a table of two byte
+    // planes, byte e of {tl1:tl0} the low byte of entry e, of {th1:th0} its high byte. The
+    // codebook entries are staged as selectors e (stage_iq3s_sel), so one v_perm per plane
+    // gathers the four values of a codebook entry and two more interleave them into bf16
+    // pairs: 8 VALU per four values with the signs, against 14 for convert, scale and pack.
+    uint32_t pw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pw[i] = f2bf2(db * (float)(4 * i + 1), db * (float)(4 * i + 3));
+    const uint32_t tl0 = __builtin_amdgcn_perm(pw[1], pw[0], 0x06040200u);
+    const uint32_t th0 = __builtin_amdgcn_perm(pw[1], pw[0], 0x07050301u);
+    const uint32_t tl1 = __builtin_amdgcn_perm(pw[3], pw[2], 0x06040200u);
+    const uint32_t th1 = __builtin_amdgcn_perm(pw[3], pw[2], 0x07050301u);
+    // value 4k + j takes sign bit 4k + j of sg. (sign ? -v : v) of v = db * m flips the sign
+    // bit of v, and so of its bf16 rounding: bits 2p and 2p + 1 of sg are moved to bits 15
+    // and 31 of the packed pair of values 2p, 2p + 1 by one packed 16-bit shift of sg's
+    // half-word (in both halves) and xored in
     const uint32_t sgw[2] = {(sg & 0xFFFFu) | (sg << 16), (sg >> 16) | (sg & 0xFFFF0000u)};
     auto pair_signs = [&](int pr) {
       const int q = (2 * pr) & 15;
@@ -357,11 +389,10 @@ struct BPiece<GGML_IQ3_S> {
     };
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      float y[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) y[j] = db * (float)((lk.g[k] >> (8 * j)) & 0xFF);
-      out[2 * k] = f2bf2(y[0], y[1]) ^ pair_signs(2 * k);
-      out[2 * k + 1] = f2bf2(y[2], y[3]) ^ pair_signs(2 * k + 1);
+      const uint32_t lo = __builtin_amdgcn_perm(tl1, tl0, lk.g[k]);  // low bytes of values 0..3
+      const uint32_t hi = __builtin_amdgcn_perm(th1, th0, lk.g[k]);  // their high bytes
+      out[2 * k] = __builtin_amdgcn_perm(hi, lo, 0x05010400u) ^ pair_signs(2 * k);
+      out[2 * k + 1] = __builtin_amdgcn_perm(hi, lo, 0x07030602u) ^ pair_signs(2 * k + 1);
     }
   }
   template <int S2>

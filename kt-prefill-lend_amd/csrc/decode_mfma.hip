@@ -192,7 +192,7 @@ __global__ __launch_bounds__(DM_THREADS) void dm_gate_up(const uint16_t* __restr
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int G = N / DM_RT;
   const int kslot = blockIdx.x / G, rg = blockIdx.x - kslot * G;
-  if constexpr (TYPE == GGML_IQ3_S) stage_iq3s_grid(grid);
+  if constexpr (TYPE == GGML_IQ3_S) stage_iq3s_sel(grid);
   WaveRoutes wr;
   wr.load(slot_ids, R, S);
   SlotSet ss;
@@ -344,7 +344,7 @@ __global__ __launch_bounds__(DN_THREADS) void dm_down(const uint16_t* __restrict
   const int ntile = K / DN_TILE;
   const int kslot = blockIdx.x / ntile, tile = blockIdx.x - kslot * ntile;
   const int c0 = tile * DN_TILE;
-  if constexpr (TYPE == GGML_IQ3_S) stage_iq3s_grid(grid);
+  if constexpr (TYPE == GGML_IQ3_S) stage_iq3s_sel(grid);
   WaveRoutes wr;
   wr.load(slot_ids, R, S);
   SlotSet ss;

@@ -43,7 +43,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
   using BP = BPiece<TYPE>;
   __shared__ uint32_t grid[TYPE == GGML_IQ3_S ? 512 : 1];
   if constexpr (TYPE == GGML_IQ3_S) {
-    stage_iq3s_grid(grid);
+    stage_iq3s_sel(grid);
     __syncthreads();
   }
   const int64_t e = blockIdx.y;

@@ -40,4 +40,11 @@ __device__ __forceinline__ void stage_iq3s_grid(uint32_t* lds_grid) {
   for (int i = threadIdx.x; i < 512; i += blockDim.x) lds_grid[i] = c_iq3s_grid[i];
 }
 
+// the codebook as byte selectors (one workgroup, call before a __syncthreads()): byte b of
+// entry i is (m - 1) / 2 = m >> 1 for the magnitude m of the codebook's byte, the position
+// 0..7 of m among the eight odd magnitudes 1..15 (the B-piece decoder's v_perm tables)
+__device__ __forceinline__ void stage_iq3s_sel(uint32_t* lds_sel) {
+  for (int i = threadIdx.x; i < 512; i += blockDim.x) lds_sel[i] = (c_iq3s_grid[i] >> 1) & 0x07070707u;
+}
+
 }  // namespace ktmi

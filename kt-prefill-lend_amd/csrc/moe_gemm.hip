@@ -266,9 +266,10 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
   constexpr int A_BYTES = BM * A_ROW;
   constexpr int AJ = A_BYTES / (16 * NTHREADS);  // direct loads per thread per step
   static_assert(AJ % 2 == 0, "A loads are spread over the 2 regions of a step");
-  // one LDS object: the IQ3_S codebook sits behind the activation buffers. With a second
+  // one LDS object: the IQ3_S codebook, then the activation buffers. With a second
   // __shared__ variable the compiler tracks the direct buffer->LDS loads per object and
-  // waits for all of them (vmcnt(0)) before every LDS read, which drains the prefetch.
+  // waits for all of them (vmcnt(0)) before every LDS read, which drains the prefetch. The
+  // codebook's offset 0 lets each lookup take its address straight from the index (no add).
   constexpr int GRID_BYTES = TYPE == GGML_IQ3_S ? 512 * 4 : 0;
   constexpr int OROW_BYTES = GATEUP ? 0 : BM * 4;  // down: the tile's output row indices
   // 256-route tiles (one block per CU, LDS to spare): each wave stages its own 32-route slices
@@ -278,8 +279,9 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
   constexpr int STG_WAVE = 32 * STG_COLS * 2;                // 32 routes of them, bf16
   constexpr int STG_BYTES = WAVE_STG ? NWAVES * STG_WAVE : 0;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[AD * A_BYTES + GRID_BYTES + OROW_BYTES + STG_BYTES];
-  uint32_t* const grid_lds = (uint32_t*)(smem + AD * A_BYTES);
-  int32_t* const orow_lds = (int32_t*)(smem + AD * A_BYTES + GRID_BYTES);
+  uint32_t* const grid_lds = (uint32_t*)smem;
+  uint8_t* const a_lds = smem + GRID_BYTES;  // activation buffer b at a_lds + b * A_BYTES
+  int32_t* const orow_lds = (int32_t*)(a_lds + AD * A_BYTES);
   using BP = BPiece<TYPE>;
 
   // XCD-aware order: workgroups are dealt to the 8 XCDs round-robin (pid % 8). Tile-table
@@ -296,7 +298,7 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
   const int e = ti.x, m0 = ti.y, valid = ti.z;
   if (valid == 0) return;
 
-  if constexpr (TYPE == GGML_IQ3_S) stage_iq3s_grid(grid_lds);
+  if constexpr (TYPE == GGML_IQ3_S) stage_iq3s_sel(grid_lds);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -331,7 +333,7 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
     const int sbase = 2 * (256 * sb + BP::template ksub<SUB>());
 #pragma unroll
     for (int j = j0; j < j1; ++j) {
-      uint8_t* dst = smem + buf * A_BYTES + (8 * (NWAVES * j + wave)) * A_ROW;
+      uint8_t* dst = a_lds + buf * A_BYTES + (8 * (NWAVES * j + wave)) * A_ROW;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (__attribute__((address_space(3))) void*)dst, 16, (int)a_off[j],
                                                sbase, 0, 0);
     }
@@ -419,7 +421,7 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
     }
     int anext = abuf + AD - 1;
     if (anext >= AD) anext -= AD;
-    const uint8_t* Ab = smem + abuf * A_BYTES;
+    const uint8_t* Ab = a_lds + abuf * A_BYTES;
     // two regions of two sub-steps; in each: half of the direct loads of A(k+3), the raw
     // bytes of one piece of step k+2 (raw[cur] held step k, decoded one step ago), the
     // reads of the next sub-steps' activation operands (double-buffered in registers), 32
@@ -504,7 +506,7 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
   constexpr int CCOLS = GATEUP ? BNW / 2 : BNW;  // output columns of a tile
   constexpr int CW = CCOLS / 8;                  // 16-byte chunks per row
   static_assert(BM * CCOLS * 2 <= AD * A_BYTES, "C tile fits the activation buffers");
-  uint8_t* cs = smem;
+  uint8_t* cs = a_lds;
   auto c_put = [&](int row, int col, uint32_t lo, uint32_t hi) {
     const int c = col >> 3;
     u32x2_t v = {lo, hi};
@@ -522,7 +524,7 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
       // wave's LDS operations complete in order, so no barrier sits between the writes and
       // the reads of other lanes, nor between the reads and the next slice's writes.
       __builtin_amdgcn_s_waitcnt(0);  // the clamped prefetches of the last steps (into LDS) have landed
-      uint8_t* stg = smem + AD * A_BYTES + GRID_BYTES + OROW_BYTES + wave * STG_WAVE;
+      uint8_t* stg = a_lds + AD * A_BYTES + OROW_BYTES + wave * STG_WAVE;
       const __amdgpu_buffer_rsrc_t y_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)out, (short)0, out_bytes, 0x00020000);
       const uint32_t col_b = 2u * (uint32_t)(nt * CCOLS + wn * FI * 32) + 16u * (uint32_t)(lane & 7);
 #pragma unroll
@@ -605,7 +607,7 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
     // waves write the rest of each H row segment)
     static_assert(FH == 1, "one gate and one up fragment per wave");
     __builtin_amdgcn_s_waitcnt(0);  // the clamped prefetches of the last steps (into LDS) have landed
-    uint8_t* stg = smem + AD * A_BYTES + GRID_BYTES + OROW_BYTES + wave * STG_WAVE;
+    uint8_t* stg = a_lds + AD * A_BYTES + OROW_BYTES + wave * STG_WAVE;
     auto sw = [](int r) { return ((r >> 1) ^ (r >> 3)) & 3; };
     const __amdgpu_buffer_rsrc_t h_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)out, (short)0, out_bytes, 0x00020000);
     const uint32_t col_b = 2u * (uint32_t)(nt * CCOLS + wn * 32) + 16u * (uint32_t)(lane & 3);
