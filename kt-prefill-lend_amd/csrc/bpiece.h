@@ -115,11 +115,18 @@ struct NoLookup {
   __device__ static void decode(const Head& hd, const Raw& r, const uint32_t* grid, uint32_t out[16]) {
     P::template decode_hp<SUB / 2>(hd, r, grid, SUB & 1, out);
   }
+  // load<SUB> for a kernel that holds the raw bytes of step SUB - 1 of the same super-block
+  // in `prev` (a format whose step pairs share bytes takes them from there)
+  template <int SUB, class Raw>
+  __device__ static void load_next(const uint8_t* row, int sb, int h, const uint32_t* grid, Raw& r, const Raw&) {
+    P::template load_hp<SUB / 2>(row, sb, h, SUB & 1, grid, r);
+  }
 };
 
 template <>
 struct BPiece<GGML_Q4_K> : NoLookup<BPiece<GGML_Q4_K>> {
   static constexpr int NLOAD = 1;  // VMEM instructions per load<SUB>, at least
+  static constexpr int NLOAD2 = 2;  // VMEM instructions of load_next over two consecutive steps
   static constexpr int VPM = 4;    // VALU instructions the GEMM schedule places after each MFMA
   struct Head { u32x4_t hdr; };  // d, dmin, scales[12]
   struct Raw { u32x4_t q; };
@@ -169,6 +176,7 @@ struct BPiece<GGML_Q4_K> : NoLookup<BPiece<GGML_Q4_K>> {
 template <>
 struct BPiece<GGML_Q8_0> : NoLookup<BPiece<GGML_Q8_0>> {
   static constexpr int NLOAD = 3;  // VMEM instructions per load<SUB>, at least
+  static constexpr int NLOAD2 = 6;  // VMEM instructions of load_next over two consecutive steps
   static constexpr int VPM = 4;    // VALU instructions the GEMM schedule places after each MFMA
   struct Head {};
   struct Raw { uint32_t w[9]; uint32_t s; };
@@ -211,6 +219,9 @@ struct BPiece<GGML_Q8_0> : NoLookup<BPiece<GGML_Q8_0>> {
 template <>
 struct BPiece<GGML_Q6_K> : NoLookup<BPiece<GGML_Q6_K>> {
   static constexpr int NLOAD = 4;  // VMEM instructions per load<SUB>, at least
+  // VMEM instructions of load_next over two consecutive steps: the odd step of a pair loads
+  // only its ql bytes (the pair's qh bytes are the same)
+  static constexpr int NLOAD2 = 6;
   static constexpr int VPM = 5;    // VALU instructions the GEMM schedule places after each MFMA
   // the 20 bytes from the dword below scales[0]: scales[16] and d, s = byte shift
   struct Head { uint32_t w[5]; uint32_t s; };
@@ -246,6 +257,23 @@ struct BPiece<GGML_Q6_K> : NoLookup<BPiece<GGML_Q6_K>> {
     }
     r.ql[4] = M::template ld<uint32_t>(ql + 4);
     r.qh[4] = M::template ld<uint32_t>(qh + 4);
+  }
+  // steps 2 hh and 2 hh + 1 read the same 16 qh bytes (bits 2c.. of run c, c = SUB & 1): the
+  // odd step takes them from the even one's raw bytes and loads only its ql bytes
+  template <int SUB>
+  __device__ __forceinline__ static void load_next(const uint8_t* row, int sb, int h, const uint32_t* grid, Raw& r,
+                                                   const Raw& prev) {
+    if constexpr ((SUB & 1) == 0) {
+      load_hp<SUB / 2>(row, sb, h, 0, grid, r);
+    } else {
+      const uint32_t* ql = dword_floor(row + sb * QB6_K + 64 * (SUB / 2) + 32 + 16 * h);
+      const u32x4_t l4 = GMem::ld<u32x4_a4_t>(ql);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r.ql[i] = l4[i];
+      r.ql[4] = GMem::ld<uint32_t>(ql + 4);
+#pragma unroll
+      for (int i = 0; i < 5; ++i) r.qh[i] = prev.qh[i];
+    }
   }
   template <int S2>
   __device__ __forceinline__ static void decode_hp(const Head& hd, const Raw& r, const uint32_t*, int p,
@@ -291,6 +319,7 @@ struct BPiece<GGML_IQ3_S> {
   // VMEM instructions per load<SUB>: qs (dwordx2 + dword, merged into one dwordx3), the
   // signs (dwordx2) and the qh dword
   static constexpr int NLOAD = 3;
+  static constexpr int NLOAD2 = 6;  // VMEM instructions of load_next over two consecutive steps
   static constexpr int VPM = 4;    // VALU instructions the GEMM schedule places after each MFMA
   // d and the 4 scale bytes of the block (dwords below them, realigned at decode)
   struct Head { uint32_t dw, sc0, sc1; uint32_t s; };
@@ -405,6 +434,10 @@ struct BPiece<GGML_IQ3_S> {
   // the <SUB> forms through the run-time parity bodies
   template <int SUB>
   __device__ static void load(const uint8_t* row, int sb, int h, const uint32_t* grid, Raw& r) {
+    load_hp<SUB / 2>(row, sb, h, SUB & 1, grid, r);
+  }
+  template <int SUB>
+  __device__ static void load_next(const uint8_t* row, int sb, int h, const uint32_t* grid, Raw& r, const Raw&) {
     load_hp<SUB / 2>(row, sb, h, SUB & 1, grid, r);
   }
   template <int SUB>

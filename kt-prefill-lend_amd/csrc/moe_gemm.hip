@@ -395,14 +395,14 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
     issue_a(0, S2{}, 2, 0, AJ);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < FI; ++i) BP::template load<1>(b_row[i], 0, h, grid_lds, raw[1][i]);
+    for (int i = 0; i < FI; ++i) BP::template load_next<1>(b_row[i], 0, h, grid_lds, raw[1][i], raw[0][i]);
     __builtin_amdgcn_sched_barrier(0);
   };
   prologue();
   // wait for A(0) only and decode step 0 (its raw bytes come after A(1): the compiler's wait
   // for them also covers A(1))
-  static_assert(2 * AJ + 2 * FI * BP::NLOAD < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt(wait_vmcnt(2 * AJ + 2 * FI * BP::NLOAD));
+  static_assert(2 * AJ + FI * BP::NLOAD2 < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(wait_vmcnt(2 * AJ + FI * BP::NLOAD2));
   __syncthreads();  // A(0) of every wave; the codebook
 #pragma unroll
   for (int i = 0; i < FI; ++i) BP::template decode<0>(head[i], raw[0][i], grid_lds, wv[0][i]);
@@ -442,7 +442,8 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
       BP::template lookup<SUB1>(hd1, raw[cur ^ 1][s2 / 2], grid_lds, look);
       __builtin_amdgcn_sched_barrier(0);
       issue_a(sb3, std::integral_constant<int, SUB3>{}, anext, (s2 / 2) * AJ / 2, (s2 / 2 + 1) * AJ / 2);
-      BP::template load<SUB2>(b_row[s2 / 2], sb2, h, grid_lds, raw[cur][s2 / 2]);
+      // raw[cur ^ 1] holds step k+1, the step before k+2 in the same super-block column
+      BP::template load_next<SUB2>(b_row[s2 / 2], sb2, h, grid_lds, raw[cur][s2 / 2], raw[cur ^ 1][s2 / 2]);
 #pragma unroll
       for (int j = 0; j < FJ; ++j) af[1][j] = *(const bf16x8_t*)(Ab + j * 32 * A_ROW + a_rd[s2 + 1]);
 #pragma unroll
@@ -483,10 +484,11 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
       __builtin_amdgcn_sched_barrier(0);
     }
     // A(k+1) has landed once at most the VMEM ops issued after it are outstanding: A(k+2),
-    // A(k+3) and the raw bytes of steps k+1 and k+2 (NLOAD instructions a piece, the count
-    // the compiler emits; the compiler waits for those register loads itself before their
-    // decode). tests/test_asm_waitcnt.py checks this count against the gfx950 assembly.
-    constexpr int NYOUNG = 2 * (AJ + FI * BP::NLOAD);
+    // A(k+3) and the raw bytes of steps k+1 and k+2 (NLOAD2 instructions a piece over the
+    // two, the count the compiler emits; the compiler waits for those register loads itself
+    // before their decode). tests/test_asm_waitcnt.py checks this count against the gfx950
+    // assembly.
+    constexpr int NYOUNG = 2 * AJ + FI * BP::NLOAD2;
     static_assert(NYOUNG < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt(wait_vmcnt(NYOUNG));
     lds_barrier();
