@@ -39,7 +39,8 @@ constexpr int MAX_SLOTS = 512;
 // columns). The weights never touch LDS: each lane loads the raw GGUF bytes of its FI rows
 // and decodes them straight into MFMA operand registers; LDS holds only the activation
 // tile. FJ is a kernel parameter: 8 (256-route tiles) for long chunks, 4 (128 routes) when
-// 256-route tiles would leave CUs idle (grouped_fj).
+// 256-route tiles would leave CUs idle (grouped_fj); a 256-route kernel runs a slot's last
+// tile with the 128-route body when it holds at most 128 routes.
 constexpr int BK = 64;
 constexpr int WN = 4, WM = 1;          // waves over weight rows x waves over routes
 constexpr int NWAVES = WN * WM;
@@ -256,12 +257,23 @@ constexpr int gemm_waves_per_simd() { return FJ == 8 || TYPE == GGML_Q6_K || TYP
 // out as row segments (the down GEMM's rows scatter to Y[perm[m]], whose indices the
 // prologue put in LDS): at 256-route tiles through a staging area of each wave's own, at
 // 128-route tiles through a C tile in LDS over the activation buffers.
+// LDS of one tile (one object: the IQ3_S codebook, the activation buffers, the down tile's
+// output row indices, the per-wave staging areas of 256-route tiles)
 template <int TYPE, bool GATEUP, int FJ>
-__global__ __launch_bounds__(NTHREADS, (gemm_waves_per_simd<TYPE, FJ>()))
-void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const int32_t* __restrict__ perm,
-                  const int4* __restrict__ tile_info, int top_k, const uint8_t* __restrict__ W, int w_is_table,
-                  int64_t w_expert_stride, int64_t rb, int Kdim, int NI, int NT, int64_t nblk,
-                  uint16_t* __restrict__ out, uint32_t out_bytes) {
+constexpr int gemm_lds_bytes() {
+  constexpr int STG_COLS = GATEUP ? FI / 2 * 32 : FI * 32;
+  return (TYPE == GGML_IQ3_S ? 512 * 4 : 0) + AD * tile_m<FJ>() * A_ROW + (GATEUP ? 0 : tile_m<FJ>() * 4) +
+         (FJ == 8 ? NWAVES * 32 * STG_COLS * 2 : 0);
+}
+
+// One tile: routes m0 .. m0 + valid - 1 of the slot whose weights start at wexp, weight-row
+// tile nt. smem holds at least gemm_lds_bytes<TYPE, GATEUP, FJ>() and, for IQ3_S, the staged
+// codebook at offset 0 (visible after the prologue's barrier).
+template <int TYPE, bool GATEUP, int FJ>
+__device__ __forceinline__ void gemm_tile(uint8_t* smem, const uint16_t* __restrict__ A_src, uint32_t a_bytes,
+                                          const int32_t* __restrict__ perm, int top_k,
+                                          const uint8_t* __restrict__ wexp, int64_t rb, int Kdim, int NI, int nt,
+                                          int m0, int valid, uint16_t* __restrict__ out, uint32_t out_bytes) {
   constexpr int BM = tile_m<FJ>();
   constexpr int A_BYTES = BM * A_ROW;
   constexpr int AJ = A_BYTES / (16 * NTHREADS);  // direct loads per thread per step
@@ -277,34 +289,15 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
   constexpr bool WAVE_STG = FJ == 8;
   constexpr int STG_COLS = GATEUP ? FI / 2 * 32 : FI * 32;  // the wave's output columns
   constexpr int STG_WAVE = 32 * STG_COLS * 2;                // 32 routes of them, bf16
-  constexpr int STG_BYTES = WAVE_STG ? NWAVES * STG_WAVE : 0;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[AD * A_BYTES + GRID_BYTES + OROW_BYTES + STG_BYTES];
   uint32_t* const grid_lds = (uint32_t*)smem;
   uint8_t* const a_lds = smem + GRID_BYTES;  // activation buffer b at a_lds + b * A_BYTES
   int32_t* const orow_lds = (int32_t*)(a_lds + AD * A_BYTES);
   using BP = BPiece<TYPE>;
 
-  // XCD-aware order: workgroups are dealt to the 8 XCDs round-robin (pid % 8). Tile-table
-  // position p = (idx / NT) * 8 + pid % 8 is on XCD pid % 8, and the table gives each XCD a
-  // contiguous range of (slot-sorted) M tiles, so a slot's weights are fetched into one L2;
-  // the NT N tiles of an M tile follow each other on that XCD and share the gathered rows.
-  // gridDim.x is a multiple of 8 * NT; positions without a tile hold valid = 0.
-  const int64_t pid = blockIdx.x;
-  const int64_t idx = pid >> 3;
-  const int mt = (int)((idx / NT) * 8 + (pid & 7));
-  const int nt = (int)(idx % NT);
-  if ((int64_t)mt * NT + nt >= nblk) return;
-  const int4 ti = tile_info[mt];
-  const int e = ti.x, m0 = ti.y, valid = ti.z;
-  if (valid == 0) return;
-
-  if constexpr (TYPE == GGML_IQ3_S) stage_iq3s_sel(grid_lds);
-
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wn = wave % WN, wm = wave / WN;
   const int h = lane >> 5, l32 = lane & 31;
-  const uint8_t* wexp = w_is_table ? (const uint8_t*)((const int64_t*)W)[e] : W + (int64_t)e * w_expert_stride;
 
   // ---- activation sources: direct loads, instruction j of wave w fills rows
   // 8 * (NWAVES * j + w) + lane / 8, LDS slot lane % 8
@@ -671,6 +664,43 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
     const uint32_t off = ml < valid ? (uint32_t)(m0 + ml) * (2u * (uint32_t)NI) + col_b + 16u * (uint32_t)c : 0xFFFFFFF0u;
     __builtin_amdgcn_raw_buffer_store_b128(v, h_rsrc, (int)off, 0, 0);
   }
+}
+
+// One block per (route tile, weight-row tile). A slot's last tile holds the slot's remaining
+// routes (1..BM); at 256-route tiles (FJ = 8) one that holds at most 128 runs the 128-route
+// body instead, so the padding of a slot's last tile costs at most 127 routes' MFMAs, not 255.
+template <int TYPE, bool GATEUP, int FJ>
+__global__ __launch_bounds__(NTHREADS, (gemm_waves_per_simd<TYPE, FJ>()))
+void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const int32_t* __restrict__ perm,
+                  const int4* __restrict__ tile_info, int top_k, const uint8_t* __restrict__ W, int w_is_table,
+                  int64_t w_expert_stride, int64_t rb, int Kdim, int NI, int NT, int64_t nblk,
+                  uint16_t* __restrict__ out, uint32_t out_bytes) {
+  static_assert(gemm_lds_bytes<TYPE, GATEUP, 4>() <= gemm_lds_bytes<TYPE, GATEUP, 8>(), "the 128-route body fits");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[gemm_lds_bytes<TYPE, GATEUP, FJ>()];
+
+  // XCD-aware order: workgroups are dealt to the 8 XCDs round-robin (pid % 8). Tile-table
+  // position p = (idx / NT) * 8 + pid % 8 is on XCD pid % 8, and the table gives each XCD a
+  // contiguous range of (slot-sorted) M tiles, so a slot's weights are fetched into one L2;
+  // the NT N tiles of an M tile follow each other on that XCD and share the gathered rows.
+  // gridDim.x is a multiple of 8 * NT; positions without a tile hold valid = 0.
+  const int64_t pid = blockIdx.x;
+  const int64_t idx = pid >> 3;
+  const int mt = (int)((idx / NT) * 8 + (pid & 7));
+  const int nt = (int)(idx % NT);
+  if ((int64_t)mt * NT + nt >= nblk) return;
+  const int4 ti = tile_info[mt];
+  const int e = ti.x, m0 = ti.y, valid = ti.z;
+  if (valid == 0) return;
+
+  if constexpr (TYPE == GGML_IQ3_S) stage_iq3s_sel((uint32_t*)smem);
+  const uint8_t* wexp = w_is_table ? (const uint8_t*)((const int64_t*)W)[e] : W + (int64_t)e * w_expert_stride;
+  if constexpr (FJ == 8) {
+    if (valid <= tile_m<4>()) {
+      gemm_tile<TYPE, GATEUP, 4>(smem, A_src, a_bytes, perm, top_k, wexp, rb, Kdim, NI, nt, m0, valid, out, out_bytes);
+      return;
+    }
+  }
+  gemm_tile<TYPE, GATEUP, FJ>(smem, A_src, a_bytes, perm, top_k, wexp, rb, Kdim, NI, nt, m0, valid, out, out_bytes);
 }
 
 // res[t, c] = bf16( sum_{k asc, slot_ids >= 0} fp32( bf16( Y[p, c] * bf16(w[p]) ) ) ), 8 columns

@@ -6,13 +6,15 @@ derive n from per-format load counts (BPiece<t>::NLOAD, Unit::NLD); these tests 
 sources for gfx950 and count the instructions actually emitted.
 
 * decode_gate_up: the x pieces are waited for with n <= the weight loads issued after them.
-* grouped_gemm (every type, gate/up and down, both route-tile heights): at the end of K step
-  k the activation tile of step k+1, whose direct buffer->LDS loads were issued during step
-  k-2, must have landed, so the step-end wait's n must not exceed the vector-memory
-  instructions issued after that tile's last direct load (cyclically over the 4 steps of the
-  unrolled super-block loop, and in issue order over the first super-block, which is peeled
-  off the loop, and the loop's first iteration); the prologue's own wait for tile 0
-  likewise; and no vmcnt(0) may drain the prefetch inside the K loop.
+* grouped_gemm (every type, gate/up and down, both route-tile heights; the 256-route kernels
+  also hold the 128-route body, which they run for a slot's short last tile, and every
+  K loop of a kernel is checked): at the end of K step k the activation tile of step k+1,
+  whose direct buffer->LDS loads were issued during step k-2, must have landed, so the
+  step-end wait's n must not exceed the vector-memory instructions issued after that
+  tile's last direct load (cyclically over the 4 steps of the unrolled super-block loop,
+  and in issue order over the first super-block, which is peeled off the loop, and the
+  loop's first iteration); the prologue's own wait for tile 0 likewise; and no vmcnt(0)
+  may drain the prefetch inside the K loop.
 """
 import os
 import re
@@ -59,8 +61,9 @@ def test_decode_gate_up_counted_wait_covers_the_weight_loads(tmp_path):
         assert 0 < n <= loads, (lines[st].split(":")[0], n, loads)
 
 
-def _k_loop(lines, st, end):
-    """The innermost loop holding the most MFMAs (the super-block loop)."""
+def _k_loops(lines, st, end):
+    """The K loops of a kernel: per loop body holding MFMAs, the innermost loop (the
+    super-block loop), in code order."""
     labels = {}
     for i in range(st, end):
         m = re.match(r"^(\.LBB\w+):", lines[i])
@@ -69,11 +72,10 @@ def _k_loop(lines, st, end):
     loops = []
     for i in range(st, end):
         m = re.search(r"s_cbranch_\w+\s+(\.LBB\w+)", lines[i])
-        if m and m.group(1) in labels and labels[m.group(1)] < i:
+        if m and m.group(1) in labels and labels[m.group(1)] < i and any("v_mfma" in lines[j] for j in range(labels[m.group(1)], i)):
             loops.append((labels[m.group(1)], i))
-    count = {ab: sum("v_mfma" in lines[j] for j in range(ab[0], ab[1])) for ab in loops}
-    most = max(count.values())
-    return min((ab for ab in loops if count[ab] == most), key=lambda ab: ab[1] - ab[0])
+    # drop loops that contain another one
+    return sorted(ab for ab in loops if not any(o != ab and ab[0] <= o[0] and o[1] <= ab[1] for o in loops))
 
 
 def test_grouped_gemm_counted_waits_cover_the_activation_tiles(tmp_path):
@@ -82,53 +84,58 @@ def test_grouped_gemm_counted_waits_cover_the_activation_tiles(tmp_path):
     assert len(starts) == 16  # 4 types x (gate/up, down) x (256-, 128-route tiles)
     for st in starts:
         name = lines[st].split(":")[0]
-        end = next(i for i in range(st + 1, len(lines)) if "s_endpgm" in lines[i])
-        a, b = _k_loop(lines, st, end)
-        body = lines[a:b]
-        assert not [l for l in body if re.search(r"s_waitcnt.*vmcnt\(0\)", l)], (name, "vmcnt(0) in the K loop")
-        bars = [j for j, l in enumerate(body) if l.strip() == "s_barrier"]
-        assert len(bars) == 4, (name, "4 K steps per super-block", len(bars))
-        steps, prev = [], bars[-1] - len(body)
-        for s in range(4):  # step s: the instructions after the previous step's barrier up to its own
-            steps.append([j % len(body) for j in range(prev + 1, bars[s])])
-            prev = bars[s]
-        waits = []
-        for s in range(4):
-            w = next(body[j] for j in reversed(steps[s]) if "s_waitcnt" in body[j] and "vmcnt" in body[j])
-            waits.append(_vmcnt(w))
-            k2 = steps[(s - 2) % 4]
-            dmas = [p for p, j in enumerate(k2) if DMA.match(body[j])]
-            assert dmas, (name, "no direct loads in step", (s - 2) % 4)
-            after = sum(1 for j in k2[dmas[-1] + 1:] if VMEM.match(body[j]))
-            after += sum(1 for j in steps[(s - 1) % 4] if VMEM.match(body[j]))
-            after += sum(1 for j in steps[s] if VMEM.match(body[j]))
-            assert 0 < waits[s] <= after, (name, "step", s, waits[s], after)
-        # before the loop: the prologue (3 tiles of AJ direct loads, then the wait for tile 0
-        # and a barrier) and the first super-block's 4 steps, peeled off the loop (their
-        # first MFMAs start the accumulators at 0)
-        pre = lines[st:a]
-        pbars = [j for j, l in enumerate(pre) if l.strip() == "s_barrier"]
-        assert len(pbars) == 5, (name, "the prologue's barrier + 4 peeled steps", len(pbars))
-        bar0 = pbars[0]
-        pro = pre[:bar0]
-        dmas = [j for j, l in enumerate(pro) if DMA.match(l)]
-        assert len(dmas) % 3 == 0 and dmas, (name, len(dmas))
-        aj = len(dmas) // 3
-        w0 = next(pro[j] for j in reversed(range(dmas[-1], bar0)) if "s_waitcnt" in pro[j] and "vmcnt" in pro[j])
-        after0 = sum(1 for l in pro[dmas[aj - 1] + 1:] if VMEM.match(l))
-        assert 0 < _vmcnt(w0) <= after0, (name, "prologue", _vmcnt(w0), after0)
-        # the first 8 steps as issued: the 4 peeled ones, then the loop's first iteration;
-        # step k's closing wait needs tile k + 1, loaded by the prologue (k < 2) or by step
-        # k - 2: at least that many VMEM ops must follow the tile's last direct load
-        seq = [pre[pbars[s] + 1:pbars[s + 1]] for s in range(4)] + [[body[j] for j in steps[s]] for s in range(4)]
-        for k in range(8):
-            w = next(l for l in reversed(seq[k]) if "s_waitcnt" in l and "vmcnt" in l)
-            if k < 2:
-                after = sum(1 for l in pro[dmas[(k + 2) * aj - 1] + 1:] if VMEM.match(l))
-            else:
-                src = seq[k - 2]
-                last = max(p for p, l in enumerate(src) if DMA.match(l))
-                after = sum(1 for l in src[last + 1:] if VMEM.match(l))
-            after += sum(1 for q in range(max(k - 1, 0), k + 1) for l in seq[q] if VMEM.match(l)) if k >= 2 else \
-                sum(1 for q in range(0, k + 1) for l in seq[q] if VMEM.match(l))
-            assert 0 < _vmcnt(w) <= after, (name, "step", k, _vmcnt(w), after)
+        end = next(i for i in range(st + 1, len(lines)) if lines[i].startswith(".Lfunc_end"))
+        loops = _k_loops(lines, st, end)
+        fj8 = re.search(r"grouped_gemmILi\d+ELb\dELi8E", name) is not None
+        assert len(loops) == (2 if fj8 else 1), (name, "K loops", loops)
+        for a, b in loops:
+            _check_k_loop(lines, name, a, b)
+
+
+def _check_k_loop(lines, name, a, b):
+    body = lines[a:b]
+    assert not [l for l in body if re.search(r"s_waitcnt.*vmcnt\(0\)", l)], (name, "vmcnt(0) in the K loop")
+    bars = [j for j, l in enumerate(body) if l.strip() == "s_barrier"]
+    assert len(bars) == 4, (name, "4 K steps per super-block", len(bars))
+    steps, prev = [], bars[-1] - len(body)
+    for s in range(4):  # step s: the instructions after the previous step's barrier up to its own
+        steps.append([j % len(body) for j in range(prev + 1, bars[s])])
+        prev = bars[s]
+    waits = []
+    for s in range(4):
+        w = next(body[j] for j in reversed(steps[s]) if "s_waitcnt" in body[j] and "vmcnt" in body[j])
+        waits.append(_vmcnt(w))
+        k2 = steps[(s - 2) % 4]
+        dmas = [p for p, j in enumerate(k2) if DMA.match(body[j])]
+        assert dmas, (name, "no direct loads in step", (s - 2) % 4)
+        after = sum(1 for j in k2[dmas[-1] + 1:] if VMEM.match(body[j]))
+        after += sum(1 for j in steps[(s - 1) % 4] if VMEM.match(body[j]))
+        after += sum(1 for j in steps[s] if VMEM.match(body[j]))
+        assert 0 < waits[s] <= after, (name, "step", s, waits[s], after)
+    # before the loop: the prologue (3 tiles of AJ direct loads, then the wait for tile 0
+    # and a barrier) and the first super-block's 4 steps, peeled off the loop (their
+    # first MFMAs start the accumulators at 0): the 5 barriers right before the loop
+    aj = sum(1 for l in body if DMA.match(l)) // 4
+    pb = [j for j in range(a) if lines[j].strip() == "s_barrier"][-5:]
+    assert len(pb) == 5 and aj > 0, (name, "the prologue's barrier + 4 peeled steps")
+    bar0 = pb[0]
+    dmas = [j for j in range(bar0) if DMA.match(lines[j])][-3 * aj:]
+    w0 = next(lines[j] for j in reversed(range(dmas[-1], bar0)) if "s_waitcnt" in lines[j] and "vmcnt" in lines[j])
+    after0 = sum(1 for j in range(dmas[aj - 1] + 1, bar0) if VMEM.match(lines[j]))
+    assert 0 < _vmcnt(w0) <= after0, (name, "prologue", _vmcnt(w0), after0)
+    # the first 8 steps as issued: the 4 peeled ones, then the loop's first iteration;
+    # step k's closing wait needs tile k + 1, loaded by the prologue (k < 2) or by step
+    # k - 2: at least that many VMEM ops must follow the tile's last direct load
+    seq = [lines[pb[s] + 1:pb[s + 1]] for s in range(4)] + [[body[j] for j in steps[s]] for s in range(4)]
+    pro_tail = lambda k: lines[dmas[(k + 2) * aj - 1] + 1:bar0]
+    for k in range(8):
+        w = next(l for l in reversed(seq[k]) if "s_waitcnt" in l and "vmcnt" in l)
+        if k < 2:
+            after = sum(1 for l in pro_tail(k) if VMEM.match(l))
+        else:
+            src = seq[k - 2]
+            last = max(p for p, l in enumerate(src) if DMA.match(l))
+            after = sum(1 for l in src[last + 1:] if VMEM.match(l))
+        after += sum(1 for q in range(max(k - 1, 0), k + 1) for l in seq[q] if VMEM.match(l)) if k >= 2 else \
+            sum(1 for q in range(0, k + 1) for l in seq[q] if VMEM.match(l))
+        assert 0 < _vmcnt(w) <= after, (name, "step", k, _vmcnt(w), after)
