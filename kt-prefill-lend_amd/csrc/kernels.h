@@ -56,7 +56,7 @@ struct GroupedPlan {
   int fj;              // route fragments of 32 per wave (the kernel's FJ)
   int64_t bm;          // routes per M tile (32 fj)
   // workspace carve-up (byte offsets)
-  int64_t off_counts, off_seg, off_tseg, off_tinfo, off_perm, off_h, off_y, total;
+  int64_t off_counts, off_seg, off_tseg, off_tinfo, off_perm, off_tok, off_h, off_y, total;
 };
 GroupedPlan grouped_plan(int64_t tokens, int64_t top_k, int64_t n_slots, int64_t hidden, int64_t inter);
 int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* topk_w, const int32_t* slot_ids,

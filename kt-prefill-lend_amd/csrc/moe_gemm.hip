@@ -116,7 +116,8 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_scan_chunks(int32_t* __rest
   if (threadIdx.x == 0) tot[blockIdx.x] = total;
 }
 
-// grid (nch + 3) / 4: wave w of block b scatters the routes of chunk 4b + w to perm. Every
+// grid (nch + 3) / 4: wave w of block b scatters the routes of chunk 4b + w to perm (and their
+// tokens, p / top_k, to tok: the gate/up GEMM's gathered rows, no division there). Every
 // block first scans the S slot totals itself (S <= 512, two per thread) for the slots' first
 // sorted positions and first tiles (tiles of bm routes); block 0 writes seg[S+1] (route
 // offsets) and tseg[S+1] (tile offsets). The grid's threads then fill the tile table in the
@@ -130,7 +131,8 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_scatter(const int32_t* __re
                                                              const int32_t* __restrict__ tot,
                                                              int32_t* __restrict__ seg, int32_t* __restrict__ tseg,
                                                              int4* __restrict__ tile_info, int64_t npos, int bm,
-                                                             int32_t* __restrict__ perm) {
+                                                             int top_k, int32_t* __restrict__ perm,
+                                                             int32_t* __restrict__ tok) {
   __shared__ int run[SORT_THREADS / 64][MAX_SLOTS];
   __shared__ int segl[MAX_SLOTS + 1];
   __shared__ int tsegl[MAX_SLOTS + 1];
@@ -199,6 +201,7 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_scatter(const int32_t* __re
     if (hot) {
       const int rank = __popcll(same & lt);
       perm[base + rank] = (int32_t)p;
+      tok[base + rank] = (int32_t)(p / top_k);  // the gate/up GEMM's gathered row
       if ((same & lt) == 0) run[w][e] = base + __popcll(same);  // lowest lane of the group
     }
     __builtin_amdgcn_wave_barrier();
@@ -234,7 +237,7 @@ __device__ __forceinline__ int lds_slot(int row, int chunk) { return chunk ^ (ro
 template <int TYPE, int FJ>
 constexpr int gemm_waves_per_simd() { return FJ == 8 || TYPE == GGML_Q6_K || TYPE == GGML_IQ3_S ? 1 : 2; }
 
-// GATEUP = true : activations = x rows gathered through perm (token = p / top_k),
+// GATEUP = true : activations = x rows gathered through perm (here the sorted routes' tokens),
 //                 Kdim = hidden, weight rows = [gate n0.. ; up NI+n0..], out = H [R, NI]
 //                 sorted rows, silu(gate) * up.
 // GATEUP = false: activations = H rows m0.., Kdim = inter, weight rows = down rows of the
@@ -308,7 +311,7 @@ __device__ __forceinline__ void gemm_tile(uint8_t* smem, const uint16_t* __restr
     const int chunk = lds_slot(row, lane & 7);  // the slot map is an involution per row
     const int r = min(row, valid - 1);
     int src_row;
-    if constexpr (GATEUP) src_row = perm[m0 + r] / top_k;
+    if constexpr (GATEUP) src_row = perm[m0 + r];  // the route's token (the sort's tok array)
     else src_row = m0 + r;
     a_off[j] = 2u * (uint32_t)(src_row * Kdim + BP::coff(chunk));
   }
@@ -798,6 +801,7 @@ GroupedPlan grouped_plan(int64_t tokens, int64_t top_k, int64_t n_slots, int64_t
   P.off_tseg = o; o = align256(o + (n_slots + 1) * 4);
   P.off_tinfo = o; o = align256(o + P.max_tiles * 16);
   P.off_perm = o; o = align256(o + P.routes * 4);
+  P.off_tok = o; o = align256(o + P.routes * 4);
   P.off_h = o; o = align256(o + P.routes * inter * 2);
   P.off_y = o; o = align256(o + P.routes * hidden * 2);
   P.total = o;
@@ -824,6 +828,7 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
   int32_t* seg = (int32_t*)(ws + P.off_seg);
   int32_t* tseg = (int32_t*)(ws + P.off_tseg);
   int32_t* perm = (int32_t*)(ws + P.off_perm);
+  int32_t* tok = (int32_t*)(ws + P.off_tok);
   int4* tile_info = (int4*)(ws + P.off_tinfo);
   uint16_t* H = (uint16_t*)(ws + P.off_h);
   uint16_t* Y = (uint16_t*)(ws + P.off_y);
@@ -834,7 +839,7 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
   sort_count<<<sblocks, SORT_THREADS, 0, stream>>>(slot_ids, R, S, hist, nch);
   sort_scan_chunks<<<S, SORT_THREADS, 0, stream>>>(hist, nch, tot);
   sort_scatter<<<sblocks, SORT_THREADS, 0, stream>>>(slot_ids, R, S, hist, nch, tot, seg, tseg, tile_info,
-                                                     P.max_tiles, (int)P.bm, perm);
+                                                     P.max_tiles, (int)P.bm, (int)top_k, perm, tok);
   KTMI_HIP_TRY(hipGetLastError());
   record_stage(1, stream);
   const int64_t rb13 = row_bytes(K, L->type13), rb2 = row_bytes(N, L->type2);
@@ -842,7 +847,7 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
   const int NT1 = (int)(N / (BNW / 2));
   const int64_t nblk1 = P.max_tiles * NT1;
   dim3 g1((unsigned)((nblk1 + 8 * NT1 - 1) / (8 * NT1) * (8 * NT1)));
-  int rc = dispatch_gemm<true>(L->type13, P.fj, g1, stream, x, (uint32_t)(tokens * K * 2), perm, tile_info,
+  int rc = dispatch_gemm<true>(L->type13, P.fj, g1, stream, x, (uint32_t)(tokens * K * 2), tok, tile_info,
                                (int)top_k, L->w13, L->w_is_table, st13, rb13, (int)K, (int)N, NT1, nblk1, H,
                                (uint32_t)(R * N * 2));
   if (rc) return rc;
