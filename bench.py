@@ -294,11 +294,13 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-def bench_configs(P, torch, S, ev, dev, steps=10, warmup=2):
+def bench_configs(P, torch, S, ev, dev, steps=10, warmup=2, sust_steps=50, sust_warmup=100):
     """The other prefill-sized workloads, one layer each in the mode the library picks: Q8_0
     at 512 tokens, the headline shapes at 2048 and 32768 tokens and IQ3_S at 16384. Reports
     tokens/s and the gate/up and down GEMMs' TFLOP/s against the bf16 MFMA peak (their
-    durations sampled in the timed steps)."""
+    durations sampled in the timed steps). Each leg starts from the clocks the data generation
+    left the GPU at; the long chunks (16384 tokens and more) are then timed again behind
+    `sust_warmup` back-to-back untimed steps (`sustained`: the clock state of a serving loop)."""
     H, L = P.kt_gguf_hot, P._lib
     lib = L.lib()
     cases = [("q8_0-h2048-n768-e128-k8-hot16", 512), (HEADLINE, 2048), (HEADLINE, 32768),
@@ -325,6 +327,17 @@ def bench_configs(P, torch, S, ev, dev, steps=10, warmup=2):
             if stages[k] > 0:
                 rec[f"{k}_TFLOPs"] = round(f / (stages[k] * 1e-3) / 1e12, 1)
                 rec[f"{k}_frac_mfma"] = round(f / (stages[k] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)
+        if T >= 16384 and sust_steps > 0:
+            ms2, st2, _, t2 = time_layer(P, torch, [desc], x, tw_d, slot_d, mode, sust_steps, sust_warmup, ev)
+            if t2:
+                st2 = dict(st2, gate_up=t2["gate_up"], down=t2["down"])
+            sus = {"warmup": sust_warmup, "steps": sust_steps, "ms_per_step": round(ms2, 4),
+                   "tokens_per_s": round(T / (ms2 * 1e-3), 1),
+                   "layer_frac_mfma": round((f_gu + f_dn) / (ms2 * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+            for k, f in (("gate_up", f_gu), ("down", f_dn)):
+                if st2[k] > 0:
+                    sus[f"{k}_frac_mfma"] = round(f / (st2[k] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)
+            rec["sustained"] = sus
         res[f"{name}:T{T}"] = rec
         log(f"config {name} T={T}: {rec}")
         del W13, W2, x
