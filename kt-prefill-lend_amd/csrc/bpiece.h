@@ -222,7 +222,9 @@ struct BPiece<GGML_Q6_K> : NoLookup<BPiece<GGML_Q6_K>> {
   // VMEM instructions of load_next over two consecutive steps: the odd step of a pair loads
   // only its ql bytes (the pair's qh bytes are the same)
   static constexpr int NLOAD2 = 6;
-  static constexpr int VPM = 5;    // VALU instructions the GEMM schedule places after each MFMA
+  // VALU instructions the GEMM schedule places after each MFMA: 4 for a decode of 4.1 a MFMA
+  // (headline down GEMM 255 -> 250 us at the sustained clock; 5 and 6 slower, 3 no better)
+  static constexpr int VPM = 4;
   // the 20 bytes from the dword below scales[0]: scales[16] and d, s = byte shift
   struct Head { uint32_t w[5]; uint32_t s; };
   struct Raw { uint32_t ql[5], qh[5]; };
