@@ -375,38 +375,37 @@ __device__ __forceinline__ void gemm_tile(uint8_t* smem, const uint16_t* __restr
   using S2 = std::integral_constant<int, 2>;
   using S3 = std::integral_constant<int, 3>;
 
-  // prologue in the steady state's issue order (step j issues A(j+3), then raw(j+2)):
-  // A(0), A(1), raw(0), A(2), raw(1), so that at the end of step 0 as many loads follow
-  // A(1) as at any later step (sched_barrier keeps the compiler from hoisting the register
-  // loads above the direct ones)
+  // prologue: A(0), raw(0), raw(1), all that step 0 needs before its first MFMA (step j
+  // issues A(j+3), then raw(j+2); step 0 also issues A(1) and A(2)). Issuing the loads of
+  // three activation steps here would hold the first MFMA back by their issue time, which
+  // the address unit spends at about a cycle per row touched (the Q6_K gathers most); in
+  // step 0 it runs under the MFMAs (sched_barrier keeps the compiler from hoisting the
+  // register loads above the direct ones)
   auto prologue = [&]() {
 #pragma unroll
     for (int i = 0; i < FI; ++i) BP::load_head(b_row[i], 0, h, head[i]);
     issue_a(0, S0{}, 0, 0, AJ);
-    issue_a(0, S1{}, 1, 0, AJ);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < FI; ++i) BP::template load<0>(b_row[i], 0, h, grid_lds, raw[0][i]);
-    __builtin_amdgcn_sched_barrier(0);
-    issue_a(0, S2{}, 2, 0, AJ);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < FI; ++i) BP::template load_next<1>(b_row[i], 0, h, grid_lds, raw[1][i], raw[0][i]);
     __builtin_amdgcn_sched_barrier(0);
   };
   prologue();
-  // wait for A(0) only and decode step 0 (its raw bytes come after A(1): the compiler's wait
-  // for them also covers A(1))
-  static_assert(2 * AJ + FI * BP::NLOAD2 < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt(wait_vmcnt(2 * AJ + FI * BP::NLOAD2));
+  // wait for A(0) and decode step 0 (the compiler waits for its raw bytes, issued after A(0))
+  static_assert(FI * BP::NLOAD2 < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(wait_vmcnt(FI * BP::NLOAD2));
   __syncthreads();  // A(0) of every wave; the codebook
 #pragma unroll
   for (int i = 0; i < FI; ++i) BP::template decode<0>(head[i], raw[0][i], grid_lds, wv[0][i]);
 
   int abuf = 0;
-  auto step = [&](int sb, auto subc, auto firstc) {
+  auto step = [&](int sb, auto subc, auto phasec) {
     constexpr int SUB = decltype(subc)::value;
-    constexpr bool FIRST = decltype(firstc)::value;  // the tile's first step: C starts at 0
+    constexpr int PH = decltype(phasec)::value;  // 1: the tile's first step, 2: its second, 0: later
+    constexpr bool FIRST = PH == 1;              // C starts at 0
     constexpr int cur = SUB & 1;
     constexpr int SUB1 = (SUB + 1) & 3, SUB2 = (SUB + 2) & 3, SUB3 = (SUB + 3) & 3;
     const int sb2 = SUB < 2 ? sb : min(sb + 1, lsb);
@@ -437,7 +436,19 @@ __device__ __forceinline__ void gemm_tile(uint8_t* smem, const uint16_t* __restr
       typename BP::Look look;
       BP::template lookup<SUB1>(hd1, raw[cur ^ 1][s2 / 2], grid_lds, look);
       __builtin_amdgcn_sched_barrier(0);
-      issue_a(sb3, std::integral_constant<int, SUB3>{}, anext, (s2 / 2) * AJ / 2, (s2 / 2 + 1) * AJ / 2);
+      if constexpr (FIRST) {
+        // the tile's first step issues A(1), A(2) and A(3), in that order (the prologue only
+        // A(0)): region 0 A(1) and the first half of A(2), region 1 the rest
+        if (s2 == 0) {
+          issue_a(0, S1{}, 1, 0, AJ);
+          issue_a(0, S2{}, 2, 0, AJ / 2);
+        } else {
+          issue_a(0, S2{}, 2, AJ / 2, AJ);
+          issue_a(0, S3{}, 3, 0, AJ);
+        }
+      } else {
+        issue_a(sb3, std::integral_constant<int, SUB3>{}, anext, (s2 / 2) * AJ / 2, (s2 / 2 + 1) * AJ / 2);
+      }
       // raw[cur ^ 1] holds step k+1, the step before k+2 in the same super-block column
       BP::template load_next<SUB2>(b_row[s2 / 2], sb2, h, grid_lds, raw[cur][s2 / 2], raw[cur ^ 1][s2 / 2]);
 #pragma unroll
@@ -487,7 +498,12 @@ __device__ __forceinline__ void gemm_tile(uint8_t* smem, const uint16_t* __restr
     // two, the count the compiler emits; the compiler waits for those register loads itself
     // before their decode). tests/test_asm_waitcnt.py checks this count against the gfx950
     // assembly.
-    constexpr int NYOUNG = 2 * AJ + FI * BP::NLOAD2;
+    // The tile's first two steps: A(1) is followed by A(2), A(3) and the raw bytes of step 2
+    // (at least NLOAD2 - NLOAD instructions a piece, the smaller step of a pair); A(2) by half
+    // of A(3), A(4) and step 3's raw bytes.
+    constexpr int NYOUNG = PH == 1   ? 2 * AJ + FI * (BP::NLOAD2 - BP::NLOAD)
+                           : PH == 2 ? AJ + AJ / 2 + FI * (BP::NLOAD2 - BP::NLOAD)
+                                     : 2 * AJ + FI * BP::NLOAD2;
     static_assert(NYOUNG < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt(wait_vmcnt(NYOUNG));
     lds_barrier();
@@ -584,17 +600,18 @@ __device__ __forceinline__ void gemm_tile(uint8_t* smem, const uint16_t* __restr
     }
   };
 
-  using ON = std::true_type;
-  using OFF = std::false_type;
-  step(0, S0{}, ON{});  // nsb >= 1: the layer requires Kdim to be a multiple of 256
-  step(0, S1{}, OFF{});
-  step(0, S2{}, OFF{});
-  step(0, S3{}, OFF{});
+  using P1 = std::integral_constant<int, 1>;
+  using P2 = std::integral_constant<int, 2>;
+  using P0 = std::integral_constant<int, 0>;
+  step(0, S0{}, P1{});  // nsb >= 1: the layer requires Kdim to be a multiple of 256
+  step(0, S1{}, P2{});
+  step(0, S2{}, P0{});
+  step(0, S3{}, P0{});
   for (int sb = 1; sb < nsb; ++sb) {
-    step(sb, S0{}, OFF{});
-    step(sb, S1{}, OFF{});
-    step(sb, S2{}, OFF{});
-    step(sb, S3{}, OFF{});
+    step(sb, S0{}, P0{});
+    step(sb, S1{}, P0{});
+    step(sb, S2{}, P0{});
+    step(sb, S3{}, P0{});
   }
   if constexpr (!GATEUP) {
     flush();

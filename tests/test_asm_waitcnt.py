@@ -12,9 +12,9 @@ sources for gfx950 and count the instructions actually emitted.
   whose direct buffer->LDS loads were issued during step k-2, must have landed, so the
   step-end wait's n must not exceed the vector-memory instructions issued after that
   tile's last direct load (cyclically over the 4 steps of the unrolled super-block loop,
-  and in issue order over the first super-block, which is peeled off the loop, and the
-  loop's first iteration); the prologue's own wait for tile 0 likewise; and no vmcnt(0)
-  may drain the prefetch inside the K loop.
+  and in issue order over the prologue, the first super-block, which is peeled off the
+  loop and whose first step also issues tiles 1 to 3, and the loop's first iteration);
+  and no vmcnt(0) may drain the prefetch inside the K loop.
 """
 import os
 import re
@@ -112,30 +112,27 @@ def _check_k_loop(lines, name, a, b):
         after += sum(1 for j in steps[(s - 1) % 4] if VMEM.match(body[j]))
         after += sum(1 for j in steps[s] if VMEM.match(body[j]))
         assert 0 < waits[s] <= after, (name, "step", s, waits[s], after)
-    # before the loop: the prologue (3 tiles of AJ direct loads, then the wait for tile 0
-    # and a barrier) and the first super-block's 4 steps, peeled off the loop (their
-    # first MFMAs start the accumulators at 0): the 5 barriers right before the loop
+    # before the loop: the prologue (tile 0's AJ direct loads, then its wait and a barrier)
+    # and the first super-block's 4 steps, peeled off the loop (their first MFMAs start the
+    # accumulators at 0; step 0 also issues tiles 1, 2 and 3): the 5 barriers right before
+    # the loop
     aj = sum(1 for l in body if DMA.match(l)) // 4
     pb = [j for j in range(a) if lines[j].strip() == "s_barrier"][-5:]
     assert len(pb) == 5 and aj > 0, (name, "the prologue's barrier + 4 peeled steps")
     bar0 = pb[0]
-    dmas = [j for j in range(bar0) if DMA.match(lines[j])][-3 * aj:]
-    w0 = next(lines[j] for j in reversed(range(dmas[-1], bar0)) if "s_waitcnt" in lines[j] and "vmcnt" in lines[j])
-    after0 = sum(1 for j in range(dmas[aj - 1] + 1, bar0) if VMEM.match(lines[j]))
-    assert 0 < _vmcnt(w0) <= after0, (name, "prologue", _vmcnt(w0), after0)
-    # the first 8 steps as issued: the 4 peeled ones, then the loop's first iteration;
-    # step k's closing wait needs tile k + 1, loaded by the prologue (k < 2) or by step
-    # k - 2: at least that many VMEM ops must follow the tile's last direct load
-    seq = [lines[pb[s] + 1:pb[s + 1]] for s in range(4)] + [[body[j] for j in steps[s]] for s in range(4)]
-    pro_tail = lambda k: lines[dmas[(k + 2) * aj - 1] + 1:bar0]
-    for k in range(8):
-        w = next(l for l in reversed(seq[k]) if "s_waitcnt" in l and "vmcnt" in l)
-        if k < 2:
-            after = sum(1 for l in pro_tail(k) if VMEM.match(l))
-        else:
-            src = seq[k - 2]
-            last = max(p for p, l in enumerate(src) if DMA.match(l))
-            after = sum(1 for l in src[last + 1:] if VMEM.match(l))
-        after += sum(1 for q in range(max(k - 1, 0), k + 1) for l in seq[q] if VMEM.match(l)) if k >= 2 else \
-            sum(1 for q in range(0, k + 1) for l in seq[q] if VMEM.match(l))
-        assert 0 < _vmcnt(w) <= after, (name, "step", k, _vmcnt(w), after)
+    dmas = [j for j in range(bar0) if DMA.match(lines[j])][-aj:]
+    assert len(dmas) == aj, (name, "tile 0 in the prologue")
+    # the prologue's tail from tile 0's first direct load, the 4 peeled steps, then the
+    # loop's first iteration: direct loads in tile order, aj per tile
+    pro = lines[dmas[0]:bar0]
+    seq = [pro] + [lines[pb[s] + 1:pb[s + 1]] for s in range(4)] + [[body[j] for j in steps[s]] for s in range(4)]
+    flat = [(q, l) for q, part in enumerate(seq) for l in part]
+    dma_at = [i for i, (_, l) in enumerate(flat) if DMA.match(l)]
+    assert len(dma_at) >= 9 * aj, (name, "tiles 0..8 issued by the first 8 steps", len(dma_at))
+    # seq part q >= 1 is step q - 1; its closing wait needs tile q (tile 0 for the prologue)
+    for q in range(len(seq)):
+        w_at = max(i for i, (qq, l) in enumerate(flat) if qq == q and "s_waitcnt" in l and "vmcnt" in l)
+        last = dma_at[(q + 1) * aj - 1]
+        assert last < w_at, (name, "tile", q, "issued after the wait for it")
+        after = sum(1 for i in range(last + 1, w_at) if VMEM.match(flat[i][1]))
+        assert 0 < _vmcnt(flat[w_at][1]) <= after, (name, "wait of part", q, _vmcnt(flat[w_at][1]), after)
