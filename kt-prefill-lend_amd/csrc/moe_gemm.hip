@@ -315,10 +315,13 @@ __device__ __forceinline__ void gemm_tile(uint8_t* smem, const uint16_t* __restr
     else src_row = m0 + r;
     a_off[j] = 2u * (uint32_t)(src_row * Kdim + BP::coff(chunk));
   }
-  // down: the output row of each of the tile's routes (-1 past its routes), in LDS (visible
-  // after the prologue's barrier, read by the epilogue)
+  // down: the output row of each of the tile's routes (-1 past its routes), loaded here and
+  // put in LDS once the prologue's loads are out (so they do not wait for it); visible after
+  // the prologue's barrier, read by the epilogue
+  static_assert(BM <= NTHREADS, "one output row per thread");
+  int orow_v = -1;
   if constexpr (!GATEUP) {
-    for (int ml = tid; ml < BM; ml += NTHREADS) orow_lds[ml] = ml < valid ? perm[m0 + ml] : -1;
+    if (tid < valid) orow_v = perm[m0 + tid];
   }
   // buffer loads into LDS: the step's column offset is a scalar operand, the lane's row
   // offset a fixed register, so no address arithmetic per load; reads beyond a_bytes
@@ -394,6 +397,9 @@ __device__ __forceinline__ void gemm_tile(uint8_t* smem, const uint16_t* __restr
     __builtin_amdgcn_sched_barrier(0);
   };
   prologue();
+  if constexpr (!GATEUP) {
+    if (tid < BM) orow_lds[tid] = orow_v;
+  }
   // wait for A(0) and decode step 0 (the compiler waits for its raw bytes, issued after A(0))
   static_assert(FI * BP::NLOAD2 < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt(wait_vmcnt(FI * BP::NLOAD2));
