@@ -80,7 +80,7 @@ struct LMem {
   // pointer would add a null check that the compiler here lowers wrongly)
   template <typename T>
   __device__ __forceinline__ static T ld(const void* p) {
-    return *(const __attribute__((address_space(3))) T*)(uint32_t)(uintptr_t)p;
+    return *(const __attribute__((address_space(3))) T*)(uintptr_t)(uint32_t)(uintptr_t)p;
   }
 };
 

@@ -17,6 +17,8 @@
 // their add after the wait. The pinned output is written again only after that add has
 // completed (event out_free), so back-to-back layers cannot overwrite it early. One submit
 // is outstanding at a time per engine.
+#include <immintrin.h>
+
 #include <algorithm>
 #include <atomic>
 #include <chrono>
