@@ -116,6 +116,82 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_scan_chunks(int32_t* __rest
   if (threadIdx.x == 0) tot[blockIdx.x] = total;
 }
 
+// The tile table: position p (npos of them, a multiple of 8) belongs to XCD p % 8, and XCD x
+// takes the contiguous range of tiles [x per, (x + 1) per), per = ceil(tb / 8), so a slot's
+// tiles (and weights) stay in one XCD's L2. Entry p = {slot, first sorted route, routes in the
+// tile, 0}, or all zero for a position without a tile. segl / tsegl: the slots' first sorted
+// route and first tile (S + 1 entries each); positions p0, p0 + pstride, ...
+__device__ __forceinline__ void fill_tile_table(const int* segl, const int* tsegl, int S, int tb, int bm,
+                                                int4* __restrict__ tile_info, int64_t npos, int64_t p0,
+                                                int64_t pstride) {
+  const int64_t per = ((int64_t)tb + 7) / 8;
+  for (int64_t p = p0; p < npos; p += pstride) {
+    const int64_t local = p >> 3, i = (p & 7) * per + local;
+    int4 info = int4{0, 0, 0, 0};
+    if (local < per && i < tb) {
+      // the tile's slot is the last e with tsegl[e] <= i (binary search)
+      int lo = 0, hi = S - 1;  // tsegl[lo] <= i < tsegl[hi + 1]
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (tsegl[mid] <= i) lo = mid;
+        else hi = mid - 1;
+      }
+      const int q = (int)i - tsegl[lo];
+      const int n = segl[lo + 1] - segl[lo];
+      info = int4{lo, segl[lo] + q * bm, min(bm, n - q * bm), 0};
+    }
+    tile_info[p] = info;
+  }
+}
+
+// The slot ids of chunk ch's CHW routes, CHW / 64 a lane (-1: cold, or past the routes)
+struct ChunkIds {
+  int e[CHW / 64];
+  __device__ __forceinline__ void load(const int32_t* __restrict__ slot_ids, int64_t R, int S, int64_t ch) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 0; k < CHW / 64; ++k) {
+      const int64_t p = ch * CHW + 64 * k + lane;
+      const int v = p < R ? slot_ids[p] : -1;
+      e[k] = v < S ? v : -1;
+    }
+  }
+};
+
+// One wave scatters the CHW routes of chunk ch (their slot ids in ids): run[e] (LDS, the
+// wave's own) holds the slot's next sorted position for this chunk (set by the caller); a
+// route's position is run[e] plus its rank among the lanes of its 64-route round holding the
+// same slot (ballots intersected over the slot id's bits), so the order inside a slot is the
+// route order.
+__device__ __forceinline__ void scatter_chunk(const ChunkIds& ids, int64_t ch, int* run, int top_k,
+                                              int32_t* __restrict__ perm, int32_t* __restrict__ tok) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+#pragma unroll
+  for (int k = 0; k < CHW / 64; ++k) {
+    const int64_t p = ch * CHW + 64 * k + lane;
+    const int e = ids.e[k];
+    const bool hot = e >= 0;
+    uint64_t same = __ballot(hot);
+#pragma unroll
+    for (int b = 0; b < 10; ++b) {
+      const bool bit = (e >> b) & 1;
+      const uint64_t bb = __ballot(bit);
+      same &= bit ? bb : ~bb;
+    }
+    int base = 0;
+    if (hot) base = run[e];
+    __builtin_amdgcn_wave_barrier();
+    if (hot) {
+      const int rank = __popcll(same & lt);
+      perm[base + rank] = (int32_t)p;
+      tok[base + rank] = (int32_t)(p / top_k);  // the gate/up GEMM's gathered row
+      if ((same & lt) == 0) run[e] = base + __popcll(same);  // lowest lane of the group
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
 // grid (nch + 3) / 4: wave w of block b scatters the routes of chunk 4b + w to perm (and their
 // tokens, p / top_k, to tok: the gate/up GEMM's gathered rows, no division there). Every
 // block first scans the S slot totals itself (S <= 512, two per thread) for the slots' first
@@ -154,58 +230,128 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_scatter(const int32_t* __re
     if (t == 0) { seg[S] = ta; tseg[S] = tb; }
   }
   __syncthreads();  // segl, tsegl
-  const int64_t per = ((int64_t)tb + 7) / 8;
-  for (int64_t p = (int64_t)blockIdx.x * SORT_THREADS + t; p < npos; p += (int64_t)gridDim.x * SORT_THREADS) {
-    const int64_t local = p >> 3, i = (p & 7) * per + local;
-    int4 info = int4{0, 0, 0, 0};
-    if (local < per && i < tb) {
-      // the tile's slot is the last e with tsegl[e] <= i (binary search)
-      int lo = 0, hi = S - 1;  // tsegl[lo] <= i < tsegl[hi + 1]
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (tsegl[mid] <= i) lo = mid;
-        else hi = mid - 1;
-      }
-      const int q = (int)i - tsegl[lo];
-      const int n = segl[lo + 1] - segl[lo];
-      info = int4{lo, segl[lo] + q * bm, min(bm, n - q * bm), 0};
-    }
-    tile_info[p] = info;
-  }
+  fill_tile_table(segl, tsegl, S, tb, bm, tile_info, npos, (int64_t)blockIdx.x * SORT_THREADS + t,
+                  (int64_t)gridDim.x * SORT_THREADS);
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t ch = (int64_t)blockIdx.x * (SORT_THREADS / 64) + w;
   if (ch >= nch) return;  // whole wave; no block-wide barrier below
+  ChunkIds ids;
+  ids.load(slot_ids, R, S, ch);
   for (int e = lane; e < S; e += 64) run[w][e] = segl[e] + hist[(int64_t)e * nch + ch];
   __builtin_amdgcn_wave_barrier();
-  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  const int64_t p0 = ch * CHW;
-  for (int it = 0; it < CHW; it += 64) {
-    const int64_t p = p0 + it + lane;
-    int e = -1;
-    if (p < R) {
-      e = slot_ids[p];
-      if (e >= S) e = -1;
-    }
-    const bool hot = e >= 0;
-    // lanes holding the same slot id: intersect ballots over the id's bits
-    uint64_t same = __ballot(hot);
+  scatter_chunk(ids, ch, run[w], top_k, perm, tok);
+}
+
+// Exclusive prefix sum over the SMALL_THREADS threads of a block (one value each); every
+// thread gets the total too. wsum holds SMALL_WAVES ints; ends with the block synchronised.
+constexpr int SMALL_THREADS = 1024;
+constexpr int SMALL_WAVES = SMALL_THREADS / 64;
+// chunks per wave of the one-block sort: one (4096 routes). Its scattered perm / tok stores all
+// go through one CU's address unit, so beyond that the three-launch sort, whose stores spread
+// over the CUs, is faster (2048 tokens x top-8 with four chunks a wave: 151 -> 164 us a layer;
+// 512 tokens x top-8, one chunk a wave: 82.0 -> 80.3 us)
+constexpr int SMALL_CPW = 1;
+__device__ __forceinline__ int block_scan_1024(int* wsum, int v, int& total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int inc = v;
 #pragma unroll
-    for (int b = 0; b < 10; ++b) {
-      const bool bit = (e >> b) & 1;
-      const uint64_t bb = __ballot(bit);
-      same &= bit ? bb : ~bb;
-    }
-    int base = 0;
-    if (hot) base = run[w][e];
-    __builtin_amdgcn_wave_barrier();
-    if (hot) {
-      const int rank = __popcll(same & lt);
-      perm[base + rank] = (int32_t)p;
-      tok[base + rank] = (int32_t)(p / top_k);  // the gate/up GEMM's gathered row
-      if ((same & lt) == 0) run[w][e] = base + __popcll(same);  // lowest lane of the group
-    }
-    __builtin_amdgcn_wave_barrier();
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += u;
   }
+  if (lane == 63) wsum[w] = inc;
+  __syncthreads();
+  int before = 0;
+  total = 0;
+#pragma unroll
+  for (int k = 0; k < SMALL_WAVES; ++k) {
+    const int x = wsum[k];
+    before += k < w ? x : 0;
+    total += x;
+  }
+  __syncthreads();  // wsum may be written again
+  return before + inc - v;
+}
+
+// The whole route sort of a short chunk in one block, one launch instead of three: the
+// outputs of sort_count + sort_scan_chunks + sort_scatter (perm, tok, seg, tseg, the tile
+// table), the same values. Chunk c (CHW routes) is counted and scattered by wave
+// c % SMALL_WAVES; the per-chunk counts (slot-major, then turned into each slot's prefix over
+// the chunks) and the waves' running positions live in dynamic LDS: (nch + SMALL_WAVES) x S
+// ints (sort_small_fits).
+__global__ __launch_bounds__(SMALL_THREADS) void sort_small(const int32_t* __restrict__ slot_ids, int R, int S,
+                                                            int nch, int32_t* __restrict__ seg,
+                                                            int32_t* __restrict__ tseg, int4* __restrict__ tile_info,
+                                                            int64_t npos, int bm, int top_k, int32_t* __restrict__ perm,
+                                                            int32_t* __restrict__ tok) {
+  extern __shared__ int dyn[];
+  int* const hist = dyn;              // [S][nch]
+  int* const run = dyn + S * nch;     // [SMALL_WAVES][S]
+  __shared__ int segl[MAX_SLOTS + 1];
+  __shared__ int tsegl[MAX_SLOTS + 1];
+  __shared__ int tot_l[MAX_SLOTS];
+  __shared__ int wsum[SMALL_WAVES];
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  for (int i = t; i < S * nch; i += SMALL_THREADS) hist[i] = 0;
+  // the wave's chunks w, w + SMALL_WAVES, ... (at most SMALL_CPW): their slot ids in registers
+  ChunkIds ids[SMALL_CPW];
+#pragma unroll
+  for (int c = 0; c < SMALL_CPW; ++c) ids[c].load(slot_ids, R, S, w + (int64_t)SMALL_WAVES * c);
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < SMALL_CPW; ++c) {
+    const int ch = w + SMALL_WAVES * c;
+#pragma unroll
+    for (int k = 0; k < CHW / 64; ++k)
+      if (ids[c].e[k] >= 0) atomicAdd(&hist[ids[c].e[k] * nch + ch], 1);  // past the routes: -1
+  }
+  __syncthreads();
+  // slot e's routes' prefix over its chunks (nch <= 64: lane ch of wave e % SMALL_WAVES), its
+  // total in tot_l[e]
+  for (int e = w; e < S; e += SMALL_WAVES) {
+    const int v = lane < nch ? hist[e * nch + lane] : 0;
+    int inc = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int u = __shfl_up(inc, o, 64);
+      if (lane >= o) inc += u;
+    }
+    if (lane < nch) hist[e * nch + lane] = inc - v;
+    if (lane == 63) tot_l[e] = inc;
+  }
+  __syncthreads();
+  const int a = t < S ? tot_l[t] : 0;
+  int ta, tb;
+  const int ea = block_scan_1024(wsum, a, ta);
+  const int eb = block_scan_1024(wsum, (a + bm - 1) / bm, tb);
+  if (t < S) {
+    segl[t] = seg[t] = ea;
+    tsegl[t] = tseg[t] = eb;
+  }
+  if (t == 0) {
+    segl[S] = seg[S] = ta;
+    tsegl[S] = tseg[S] = tb;
+  }
+  __syncthreads();  // segl, tsegl; the chunk prefixes
+  fill_tile_table(segl, tsegl, S, tb, bm, tile_info, npos, t, SMALL_THREADS);
+  int* const rw = run + w * S;
+#pragma unroll
+  for (int c = 0; c < SMALL_CPW; ++c) {
+    const int ch = w + SMALL_WAVES * c;
+    if (ch >= nch) break;  // uniform per wave
+    for (int e = lane; e < S; e += 64) rw[e] = segl[e] + hist[e * nch + ch];
+    __builtin_amdgcn_wave_barrier();
+    scatter_chunk(ids[c], ch, rw, top_k, perm, tok);
+  }
+}
+
+// routes up to which the one-block sort runs
+constexpr int64_t SMALL_ROUTES = (int64_t)SMALL_WAVES * SMALL_CPW * CHW;
+constexpr int SMALL_LDS = 60 * 1024;
+bool sort_small_fits(int64_t R, int64_t S) {
+  const int64_t nch = (R + CHW - 1) / CHW;
+  static_assert(SMALL_ROUTES / CHW <= 64, "one lane per chunk in the chunk scan");
+  return R <= SMALL_ROUTES && (nch + SMALL_WAVES) * S * 4 <= SMALL_LDS;
 }
 
 // silu(g) * u with the hardware reciprocal (1 ulp) in place of a division: the gate/up epilogue
@@ -862,10 +1008,15 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
   int32_t* tot = hist + nch * S;
   const unsigned sblocks = (unsigned)((nch + 3) / 4);
   record_stage(0, stream);
-  sort_count<<<sblocks, SORT_THREADS, 0, stream>>>(slot_ids, R, S, hist, nch);
-  sort_scan_chunks<<<S, SORT_THREADS, 0, stream>>>(hist, nch, tot);
-  sort_scatter<<<sblocks, SORT_THREADS, 0, stream>>>(slot_ids, R, S, hist, nch, tot, seg, tseg, tile_info,
-                                                     P.max_tiles, (int)P.bm, (int)top_k, perm, tok);
+  if (sort_small_fits(R, S)) {
+    sort_small<<<1, SMALL_THREADS, (unsigned)((nch + SMALL_WAVES) * S * 4), stream>>>(
+        slot_ids, (int)R, S, (int)nch, seg, tseg, tile_info, P.max_tiles, (int)P.bm, (int)top_k, perm, tok);
+  } else {
+    sort_count<<<sblocks, SORT_THREADS, 0, stream>>>(slot_ids, R, S, hist, nch);
+    sort_scan_chunks<<<S, SORT_THREADS, 0, stream>>>(hist, nch, tot);
+    sort_scatter<<<sblocks, SORT_THREADS, 0, stream>>>(slot_ids, R, S, hist, nch, tot, seg, tseg, tile_info,
+                                                       P.max_tiles, (int)P.bm, (int)top_k, perm, tok);
+  }
   KTMI_HIP_TRY(hipGetLastError());
   record_stage(1, stream);
   const int64_t rb13 = row_bytes(K, L->type13), rb2 = row_bytes(N, L->type2);
