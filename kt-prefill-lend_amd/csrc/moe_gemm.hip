@@ -399,12 +399,13 @@ constexpr int gemm_waves_per_simd() { return FJ == 8 || TYPE == GGML_Q6_K || TYP
 // (and, once per super-block column, the next column's scales into head_nxt); 4 sub-steps
 // of FI x FJ MFMAs on the weights decoded one step earlier and the activation buffer
 // k % AD, with the decode of step k+1 and the direct loads of activation step k+AD-1
-// spread over the sub-steps. Loads past the last step re-read the last one (clamped,
-// unused), keeping the loop branch-free.
+// spread over the sub-steps (step 0 also issues steps 1 and 2: the prologue loads only
+// step 0's activations and the first two steps' raw bytes). Loads past the last step
+// re-read the last one (clamped, unused), keeping the loop branch-free.
 //
 // Epilogue: the accumulators are converted (GATEUP: silu(gate) * up) to bf16 and written
-// out as row segments (the down GEMM's rows scatter to Y[perm[m]], whose indices the
-// prologue put in LDS): at 256-route tiles through a staging area of each wave's own, at
+// out as row segments (the down GEMM's rows scatter to Y[perm[m]], whose indices are put in
+// LDS right after the prologue): at 256-route tiles through a staging area of each wave's own, at
 // 128-route tiles through a C tile in LDS over the activation buffers.
 // LDS of one tile (one object: the IQ3_S codebook, the activation buffers, the down tile's
 // output row indices, the per-wave staging areas of 256-route tiles)
