@@ -247,6 +247,24 @@ def test_grouped_edge_cases(dev):
             assert l2 < TOL_REL_L2
 
 
+@pytest.mark.parametrize("hot", [400, 512])
+def test_grouped_sorts_agree_many_slots(dev, hot):
+    """Chunks of up to 4096 routes are sorted by one block (sort_small), longer ones by three
+    launches: the first 500 tokens of a 600-token chunk (4800 routes, three launches) equal the
+    same 500 tokens alone (4000 routes: one block with 400 slots; three launches with 512,
+    whose chunk counts exceed the one block's LDS) bit for bit, at hundreds of slots; both
+    against the fp64 FFN."""
+    L, _, _ = _pkg()
+    w, xb, tw, slot, w13, w2 = _case("q4_k+q6_k-h2048-n512-e256-k8-hot40-prefill", 600, 256, 256, hot, 1024)
+    assert len(np.unique(slot[slot >= 0])) > hot // 2
+    a = _run(dev, w, xb[:500], tw[:500], slot[:500], w13, w2, L.MODE_GROUPED)
+    b = _run(dev, w, xb, tw, slot, w13, w2, L.MODE_GROUPED)
+    assert np.array_equal(a, b[:500])
+    g, d = dequant_w(w13, w2, w.types, w.hidden, w.inter)
+    l2, _, cos = R.rel_errors(R.bf16_to_f32(b), R.ffn_reference(xb, slot, tw, g, d))
+    assert l2 < TOL_REL_L2 and cos > 0.999, (l2, cos)
+
+
 def test_grouped_past_the_combine_grid_limit(dev):
     """70000 tokens (560k routes, hidden 256): the combine runs in slices of 65535 tokens (the
     grid's y limit). Tokens past the first slice equal a call on those tokens alone, bit for
