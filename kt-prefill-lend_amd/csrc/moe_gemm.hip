@@ -880,27 +880,57 @@ void grouped_gemm(const uint16_t* __restrict__ A_src, uint32_t a_bytes, const in
 }
 
 // res[t, c] = bf16( sum_{k asc, slot_ids >= 0} fp32( bf16( Y[p, c] * bf16(w[p]) ) ) ), 8 columns
-// per thread
-__global__ __launch_bounds__(256) void combine_routes(const uint16_t* __restrict__ Y, const float* __restrict__ w,
+// per thread. The k's go in groups of 8 (then of 2 for the rest) whose Y loads are all issued
+// before the first is used: a token's rows are independent HBM reads, not round trips in a
+// row. A cold route (or k past top_k) loads from offset y_bytes, past the buffer's end: the
+// load returns zeros without touching memory and its weight is 0, so it adds +0.0f, which
+// leaves every sum as it was (the sum starts at +0.0f and is never -0.0f).
+__global__ __launch_bounds__(256) void combine_routes(const uint16_t* __restrict__ Y, uint32_t y_bytes,
+                                                      const float* __restrict__ w,
                                                       const int32_t* __restrict__ slot_ids, int S, int top_k,
                                                       int64_t K, uint16_t* __restrict__ res) {
   const int64_t t = blockIdx.y;
+  const __amdgpu_buffer_rsrc_t y_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)Y, (short)0, y_bytes, 0x00020000);
   for (int64_t c = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8; c < K; c += (int64_t)gridDim.x * blockDim.x * 8) {
     float a[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) a[i] = 0.0f;
-    for (int k = 0; k < top_k; ++k) {
-      const int64_t p = t * top_k + k;
-      const int e = slot_ids[p];
-      if (e < 0 || e >= S) continue;
-      const float wk = bf2f(f2bf(w[p]));
-      const u32x4_t v = __builtin_nontemporal_load((const u32x4_t*)(Y + p * K + c));  // read once
+    // routes k0 .. k0 + G - 1 (those past top_k only when GUARD)
+    auto group = [&](int k0, auto gc, auto guardc) {
+      constexpr int G = decltype(gc)::value;
+      const int64_t p0 = t * top_k + k0;
+      int e[G];
+      float wr[G];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        a[2 * i] += bf2f(f2bf(bf2f(v[i] & 0xFFFF) * wk));
-        a[2 * i + 1] += bf2f(f2bf(bf2f(v[i] >> 16) * wk));
+      for (int j = 0; j < G; ++j) {  // loaded first, whatever e is: a whole group's loads merge
+        const bool in = !decltype(guardc)::value || k0 + j < top_k;
+        e[j] = in ? slot_ids[p0 + j] : -1;
+        wr[j] = in ? w[p0 + j] : 0.0f;
       }
-    }
+      uint32_t off[G];
+      float wk[G];
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        const bool hot = e[j] >= 0 && e[j] < S;
+        wk[j] = hot ? bf2f(f2bf(wr[j])) : 0.0f;
+        off[j] = hot ? (uint32_t)(((p0 + j) * K + c) * 2) : y_bytes;
+      }
+      u32x4_t v[G];
+#pragma unroll
+      for (int j = 0; j < G; ++j) v[j] = __builtin_amdgcn_raw_buffer_load_b128(y_rsrc, off[j], 0, 2);  // nt: read once
+      __builtin_amdgcn_sched_barrier(0);  // all G loads issued before the first is used
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          a[2 * i] += bf2f(f2bf(bf2f(v[j][i] & 0xFFFF) * wk[j]));
+          a[2 * i + 1] += bf2f(f2bf(bf2f(v[j][i] >> 16) * wk[j]));
+        }
+      }
+    };
+    int k0 = 0;
+    for (; k0 + 8 <= top_k; k0 += 8) group(k0, std::integral_constant<int, 8>{}, std::false_type{});
+    for (; k0 < top_k; k0 += 2) group(k0, std::integral_constant<int, 2>{}, std::true_type{});
     u32x4_t o;
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[i] = f2bf2(a[2 * i], a[2 * i + 1]);
@@ -1041,8 +1071,8 @@ int launch_grouped_layer(const ktmi_layer* L, const uint16_t* x, const float* to
   for (int64_t t0 = 0; t0 < tokens; t0 += 65535) {
     const int64_t nt = tokens - t0 < 65535 ? tokens - t0 : 65535;
     dim3 gc((unsigned)((K / 8 + 255) / 256), (unsigned)nt);
-    combine_routes<<<gc, 256, 0, stream>>>(Y + t0 * top_k * K, topk_w + t0 * top_k, slot_ids + t0 * top_k, S,
-                                           (int)top_k, K, y + t0 * K);
+    combine_routes<<<gc, 256, 0, stream>>>(Y + t0 * top_k * K, (uint32_t)(nt * top_k * K * 2), topk_w + t0 * top_k,
+                                           slot_ids + t0 * top_k, S, (int)top_k, K, y + t0 * K);
   }
   record_stage(5, stream);
   KTMI_HIP_TRY(hipGetLastError());
