@@ -229,6 +229,33 @@ def test_decode_mode_random_windows(dev, seed):
         assert l2 < TOL_REL_L2 and cos > 0.999, (l2, l1, cos)
 
 
+@pytest.mark.parametrize("top_k", [1, 3, 6, 9, 12, 17])
+def test_grouped_mode_any_top_k(dev, top_k):
+    """The grouped mode at top-k that are not 8 (the combine reads k's in groups of 8, then of
+    2, a group's k's past top_k and its cold routes reading zeros): slot ids mixing hot slots,
+    -1 and ids past the table, one token naming one slot top_k times; against the fp64 FFN."""
+    L, H, S = _pkg()
+    rng = np.random.default_rng(200 + top_k)
+    T = 97
+    base = S.WORKLOADS["q4_k+q6_k-h2048-n512-e256-k8-hot40-prefill"]
+    w = replace(base, hidden=512, inter=256, hot=8, experts=32, top_k=top_k)
+    slot = rng.integers(-2, w.hot + 3, size=(T, top_k)).astype(np.int32)
+    slot[slot == -2] = -1
+    slot[1, :] = slot[1, 0] if slot[1, 0] >= 0 else 0
+    tw = rng.random((T, top_k)).astype(np.float32)
+    tw /= tw.sum(axis=1, keepdims=True)
+    xb = S.activations(w, T)
+    w13, w2 = S.slot_tensors(w)
+    got = R.bf16_to_f32(_run(dev, w, xb, tw, slot, w13, w2, L.MODE_GROUPED))
+    g, d = dequant_w(w13, w2, w.types, w.hidden, w.inter)
+    hot = np.where((slot >= 0) & (slot < w.hot), slot, -1)
+    ref = R.ffn_reference(xb, hot, tw, g, d)
+    cold = (hot < 0).all(axis=1)
+    assert np.all(got[cold] == 0)
+    l2, l1, cos = R.rel_errors(got[~cold], ref[~cold])
+    assert l2 < TOL_REL_L2 and cos > 0.999, (l2, l1, cos)
+
+
 def test_grouped_edge_cases(dev):
     """Empty slots, a single token, all-cold tokens, slots with one route."""
     L, _, _ = _pkg()
