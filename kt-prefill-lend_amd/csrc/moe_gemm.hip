@@ -79,21 +79,29 @@ __global__ __launch_bounds__(SORT_THREADS) void sort_count(const int32_t* __rest
     for (int e = lane; e < S; e += 64) hist[(int64_t)e * nch + ch] = cnt[w][e];
 }
 
-// exclusive block scan of 256 ints in LDS (returns the total)
+// exclusive scan over a block of 256 threads, one int each: buf[t] = the sum of the values of
+// threads before t; returns the total. Each wave scans its 64 values with lane shifts, one
+// barrier joins the 4 wave totals; ends with the block synchronised.
 __device__ int block_scan_256(int* buf, int v) {
-  const int t = threadIdx.x;
-  buf[t] = v;
-  __syncthreads();
-  for (int off = 1; off < 256; off <<= 1) {
-    const int a = t >= off ? buf[t - off] : 0;
-    __syncthreads();
-    buf[t] += a;
-    __syncthreads();
+  __shared__ int wsum[SORT_THREADS / 64];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  int inc = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += u;
   }
-  const int incl = buf[t];
-  const int total = buf[255];
+  if (lane == 63) wsum[w] = inc;
   __syncthreads();
-  buf[t] = incl - v;
+  int before = 0, total = 0;
+#pragma unroll
+  for (int k = 0; k < SORT_THREADS / 64; ++k) {
+    const int x = wsum[k];
+    before += k < w ? x : 0;
+    total += x;
+  }
+  buf[t] = before + inc - v;
+  __syncthreads();  // wsum may be written again; buf complete
   return total;
 }
 
