@@ -903,7 +903,7 @@ __global__ __launch_bounds__(256) void combine_routes(const uint16_t* __restrict
     float a[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) a[i] = 0.0f;
-    // routes k0 .. k0 + G - 1; with guardc true, the k's past top_k are neither read nor added
+    // routes k0 .. k0 + G - 1; with guardc true, a k past top_k reads no id or weight and is cold
     auto group = [&](int k0, auto gc, auto guardc) {
       constexpr int G = decltype(gc)::value;
       const int64_t p0 = t * top_k + k0;
