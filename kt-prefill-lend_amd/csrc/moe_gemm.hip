@@ -565,13 +565,21 @@ __device__ __forceinline__ void gemm_tile(uint8_t* smem, const uint16_t* __restr
   int abuf = 0;
   auto step = [&](int sb, auto subc, auto phasec) {
     constexpr int SUB = decltype(subc)::value;
-    constexpr int PH = decltype(phasec)::value;  // 1: the tile's first step, 2: its second, 0: later
-    constexpr bool FIRST = PH == 1;              // C starts at 0
+    // 1: the tile's first step, 2: its second, 3: one of its last three (with SUB 1..3), 0: any
+    // other
+    constexpr int PH = decltype(phasec)::value;
+    constexpr bool FIRST = PH == 1;  // C starts at 0
+    // the last three steps: no loads for steps past the tile's last (L = 4 nsb - 1): step k
+    // issues A(k+3) only up to k = L - 3, the raw bytes of step k+2 up to k = L - 2, the next
+    // super-block's shared bytes not at all, and the last step decodes nothing
+    constexpr bool TAIL = PH == 3;
+    static_assert(!TAIL || SUB >= 1, "tail steps are the super-block's last three");
+    constexpr bool LOAD_A = !(TAIL && SUB >= 1), LOAD_RAW = !(TAIL && SUB >= 2), DECODE = !(TAIL && SUB == 3);
     constexpr int cur = SUB & 1;
     constexpr int SUB1 = (SUB + 1) & 3, SUB2 = (SUB + 2) & 3, SUB3 = (SUB + 3) & 3;
     const int sb2 = SUB < 2 ? sb : min(sb + 1, lsb);
     const int sb3 = SUB < 1 ? sb : min(sb + 1, lsb);
-    if constexpr (SUB == 1) {
+    if constexpr (SUB == 1 && !TAIL) {
 #pragma unroll
       for (int i = 0; i < FI; ++i) BP::load_head(b_row[i], min(sb + 1, lsb), h, head_nxt[i]);
     }
@@ -595,7 +603,7 @@ __device__ __forceinline__ void gemm_tile(uint8_t* smem, const uint16_t* __restr
       // activation reads: the decode then waits only for them, not for every LDS read
       const typename BP::Head& hd1 = SUB == 3 ? head_nxt[s2 / 2] : head[s2 / 2];
       typename BP::Look look;
-      BP::template lookup<SUB1>(hd1, raw[cur ^ 1][s2 / 2], grid_lds, look);
+      if constexpr (DECODE) BP::template lookup<SUB1>(hd1, raw[cur ^ 1][s2 / 2], grid_lds, look);
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (FIRST) {
         // the tile's first step issues A(1), A(2) and A(3), in that order (the prologue only
@@ -607,11 +615,12 @@ __device__ __forceinline__ void gemm_tile(uint8_t* smem, const uint16_t* __restr
           issue_a(0, S2{}, 2, AJ / 2, AJ);
           issue_a(0, S3{}, 3, 0, AJ);
         }
-      } else {
+      } else if constexpr (LOAD_A) {
         issue_a(sb3, std::integral_constant<int, SUB3>{}, anext, (s2 / 2) * AJ / 2, (s2 / 2 + 1) * AJ / 2);
       }
       // raw[cur ^ 1] holds step k+1, the step before k+2 in the same super-block column
-      BP::template load_next<SUB2>(b_row[s2 / 2], sb2, h, grid_lds, raw[cur][s2 / 2], raw[cur ^ 1][s2 / 2]);
+      if constexpr (LOAD_RAW)
+        BP::template load_next<SUB2>(b_row[s2 / 2], sb2, h, grid_lds, raw[cur][s2 / 2], raw[cur ^ 1][s2 / 2]);
 #pragma unroll
       for (int j = 0; j < FJ; ++j) af[1][j] = *(const bf16x8_t*)(Ab + j * 32 * A_ROW + a_rd[s2 + 1]);
 #pragma unroll
@@ -634,7 +643,7 @@ __device__ __forceinline__ void gemm_tile(uint8_t* smem, const uint16_t* __restr
           for (int j = 0; j < FJ; ++j) af[0][j] = *(const bf16x8_t*)(Ab + j * 32 * A_ROW + a_rd[2]);
         }
       }
-      BP::template convert<SUB1>(hd1, raw[cur ^ 1][s2 / 2], grid_lds, look, wv[cur ^ 1][s2 / 2]);
+      if constexpr (DECODE) BP::template convert<SUB1>(hd1, raw[cur ^ 1][s2 / 2], grid_lds, look, wv[cur ^ 1][s2 / 2]);
       // schedule: the direct loads first, then 32 x (1 MFMA, VPM VALU), an LDS read after
       // every other MFMA and one of the raw weight gathers after every other (each
       // gathers 32 rows' cache lines: in one burst they would hold up the MFMA issue).
@@ -661,13 +670,19 @@ __device__ __forceinline__ void gemm_tile(uint8_t* smem, const uint16_t* __restr
     // assembly.
     // The tile's first two steps: A(1) is followed by A(2), A(3) and the raw bytes of step 2
     // (at least NLOAD2 - NLOAD instructions a piece, the smaller step of a pair); A(2) by half
-    // of A(3), A(4) and step 3's raw bytes.
+    // of A(3), A(4) and step 3's raw bytes. The last three: A(L-1) by A(L) and the raw bytes
+    // of steps L-1 and L; A(L) by step L's raw bytes; after step L nothing is waited for here
+    // and no barrier taken (every epilogue waits for its loads itself, and the ones that reuse
+    // the activation buffers synchronise the block first).
     constexpr int NYOUNG = PH == 1   ? 2 * AJ + FI * (BP::NLOAD2 - BP::NLOAD)
                            : PH == 2 ? AJ + AJ / 2 + FI * (BP::NLOAD2 - BP::NLOAD)
+                           : TAIL    ? (SUB == 1 ? AJ + FI * BP::NLOAD2 : FI * (BP::NLOAD2 - BP::NLOAD))
                                      : 2 * AJ + FI * BP::NLOAD2;
-    static_assert(NYOUNG < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt(wait_vmcnt(NYOUNG));
-    lds_barrier();
+    static_assert(NYOUNG > 0 && NYOUNG < 64, "vmcnt range");
+    if constexpr (!(TAIL && SUB == 3)) {
+      __builtin_amdgcn_s_waitcnt(wait_vmcnt(NYOUNG));
+      lds_barrier();
+    }
     abuf = abuf + 1 == AD ? 0 : abuf + 1;
     if constexpr (SUB == 3) {
 #pragma unroll
@@ -764,15 +779,22 @@ __device__ __forceinline__ void gemm_tile(uint8_t* smem, const uint16_t* __restr
   using P1 = std::integral_constant<int, 1>;
   using P2 = std::integral_constant<int, 2>;
   using P0 = std::integral_constant<int, 0>;
+  using P3 = std::integral_constant<int, 3>;
   step(0, S0{}, P1{});  // nsb >= 1: the layer requires Kdim to be a multiple of 256
   step(0, S1{}, P2{});
   step(0, S2{}, P0{});
   step(0, S3{}, P0{});
-  for (int sb = 1; sb < nsb; ++sb) {
-    step(sb, S0{}, P0{});
-    step(sb, S1{}, P0{});
-    step(sb, S2{}, P0{});
-    step(sb, S3{}, P0{});
+  if (nsb > 1) {  // (a one-column tile keeps the clamped loads of its last steps)
+    for (int sb = 1; sb < lsb; ++sb) {
+      step(sb, S0{}, P0{});
+      step(sb, S1{}, P0{});
+      step(sb, S2{}, P0{});
+      step(sb, S3{}, P0{});
+    }
+    step(lsb, S0{}, P0{});
+    step(lsb, S1{}, P3{});
+    step(lsb, S2{}, P3{});
+    step(lsb, S3{}, P3{});
   }
   if constexpr (!GATEUP) {
     flush();

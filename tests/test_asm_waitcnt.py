@@ -14,7 +14,11 @@ sources for gfx950 and count the instructions actually emitted.
   tile's last direct load (cyclically over the 4 steps of the unrolled super-block loop,
   and in issue order over the prologue, the first super-block, which is peeled off the
   loop and whose first step also issues tiles 1 to 3, and the loop's first iteration);
-  and no vmcnt(0) may drain the prefetch inside the K loop.
+  and no vmcnt(0) may drain the prefetch inside the K loop. The last super-block is peeled
+  off after the loop: its first step is an ordinary one, the three after it issue no direct
+  loads (their tiles would be past the tile's K), and the waits of its first three steps are
+  checked the same way, after the loop's last iteration and after the peeled first
+  super-block (a two-column tile runs no loop iteration).
 """
 import os
 import re
@@ -90,6 +94,7 @@ def test_grouped_gemm_counted_waits_cover_the_activation_tiles(tmp_path):
         assert len(loops) == (2 if fj8 else 1), (name, "K loops", loops)
         for a, b in loops:
             _check_k_loop(lines, name, a, b)
+            _check_last_super_block(lines, name, a, b)
 
 
 def _check_k_loop(lines, name, a, b):
@@ -136,3 +141,36 @@ def _check_k_loop(lines, name, a, b):
         assert last < w_at, (name, "tile", q, "issued after the wait for it")
         after = sum(1 for i in range(last + 1, w_at) if VMEM.match(flat[i][1]))
         assert 0 < _vmcnt(flat[w_at][1]) <= after, (name, "wait of part", q, _vmcnt(flat[w_at][1]), after)
+
+
+def _steps_of_loop(lines, a, b):
+    body = lines[a:b]
+    bars = [j for j, l in enumerate(body) if l.strip() == "s_barrier"]
+    steps, prev = [], bars[-1] - len(body)
+    for s in range(4):
+        steps.append([body[j % len(body)] for j in range(prev + 1, bars[s])])
+        prev = bars[s]
+    return steps
+
+
+def _check_last_super_block(lines, name, a, b):
+    """The peeled last super-block after the K loop (see the module docstring): its steps'
+    closing waits, with the loop's last iteration or the peeled first super-block before it."""
+    tb = [j for j in range(b + 1, len(lines)) if lines[j].strip() == "s_barrier"][:3]
+    assert len(tb) == 3, (name, "3 barriers after the loop")
+    tail = [lines[b + 1:tb[0]], lines[tb[0] + 1:tb[1]], lines[tb[1] + 1:tb[2]]]
+    aj = sum(1 for l in lines[a:b] if DMA.match(l)) // 4
+    assert [sum(1 for l in st if DMA.match(l)) for st in tail] == [aj, 0, 0], (name, "direct loads of the last steps")
+    assert all(any("v_mfma" in l for l in st) for st in tail), (name, "MFMAs in the last steps")
+    pb = [j for j in range(a) if lines[j].strip() == "s_barrier"][-5:]
+    first = [lines[pb[s] + 1:pb[s + 1]] for s in range(4)]
+    for pred in (_steps_of_loop(lines, a, b), first):
+        seq = pred + tail
+        for s in range(3):  # tail step s (sequence index 4 + s) needs the tile issued at index 2 + s
+            flat = [l for part in seq[2 + s:4 + s] for l in part] + seq[4 + s]
+            src = seq[2 + s]
+            dmas = [i for i, l in enumerate(src) if DMA.match(l)]
+            assert dmas, (name, "tail step", s, "no tile issued two steps before")
+            w_at = max(i for i, l in enumerate(flat) if "s_waitcnt" in l and "vmcnt" in l)
+            after = sum(1 for i in range(dmas[-1] + 1, w_at) if VMEM.match(flat[i]))
+            assert 0 < _vmcnt(flat[w_at]) <= after, (name, "tail step", s, _vmcnt(flat[w_at]), after)
